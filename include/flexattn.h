@@ -1,0 +1,111 @@
+/*
+ * flexattn.h — C ABI of the MI355X (gfx950) FlexAttention library
+ * (libflexattn.so).  Plain pointers and sizes only; every entry point is
+ * asynchronous on the HIP stream it is given, allocates nothing, and returns
+ * an int status (0 = success, negative = error; see fa_strerror).
+ *
+ * Which reference interface each entry point replaces (reference package
+ * src/pallas_flexattn/):
+ *   fa_fwd  — the forward pl.pallas_call of flash_attention_fwd
+ *             (flash_attn.py:111-165, kernel :59-108): O and log-sum-exp.
+ *   fa_bwd  — the three backward pl.pallas_calls of flash_attention_bwd
+ *             (flash_attn.py:410-461: preprocess :168-203, dK/dV :206-310,
+ *             dQ :313-407): dQ, dK, dV.
+ *   fa_bwd_workspace_bytes — scratch size for fa_bwd (XLA allocated the
+ *             reference's intermediates, e.g. the Delta array of :188-202).
+ *   fa_strerror / fa_abi_version — error text and ABI version for the
+ *             binding layer (no reference counterpart: the reference raised
+ *             Python exceptions at trace time).
+ *
+ * Layouts: q, o, dq are (B, Hq, Sq, D) row-major; k, v, dk, dv are
+ * (B, Hkv, Skv, D); lse is (B, Hq, Sq) float32 in natural-log units.
+ * Grouped-query attention: q head h reads kv head h / (Hq / Hkv).
+ */
+#ifndef FLEXATTN_H_
+#define FLEXATTN_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FA_ABI_VERSION 1
+
+enum fa_dtype { FA_DTYPE_BF16 = 0, FA_DTYPE_F32 = 1 };
+
+enum fa_status {
+  FA_OK = 0,
+  FA_ERR_NULL = -1,          /* a required pointer is null */
+  FA_ERR_SHAPE = -2,         /* a size is out of range or inconsistent */
+  FA_ERR_DTYPE = -3,         /* unknown dtype */
+  FA_ERR_UNSUPPORTED = -4,   /* no kernel for this head dim / tile config */
+  FA_ERR_TABLES = -5,        /* block tables inconsistent with the sizes */
+  FA_ERR_WORKSPACE = -6,     /* workspace missing or too small */
+  FA_ERR_LAUNCH = -7,        /* the HIP launch failed */
+  FA_ERR_VERSION = -8        /* params.abi_version != FA_ABI_VERSION */
+};
+
+/*
+ * Problem description.  Mask semantics (element (q, kv) is kept iff):
+ *   (window_left  < 0 || q - kv <= window_left) &&
+ *   (window_right < 0 || kv - q <= window_right) &&
+ *   (q_doc_ids == NULL || q_doc_ids[b][q] == kv_doc_ids[b][kv])
+ * causal = (-1, 0); bidirectional = (-1, -1) (mask_mod.py:15-43).
+ * Score modification, applied to s = scale * q.k before the mask:
+ *   s += alibi_slopes[h] * (kv - q)            if alibi_slopes != NULL
+ *   s  = softcap * tanh(s / softcap)          if softcap > 0
+ *
+ * Block tables (optional; all NULL = iterate every block) follow the
+ * PyTorch BlockMask convention at mask-block granularity:
+ *   kv_num_blocks[tb][th][i], kv_indices[tb][th][i][kv_width]      partial kv blocks of q block i
+ *   full_kv_num_blocks / full_kv_indices                             fully-live kv blocks of q block i
+ *   q_num_blocks[tb][th][j], q_indices[tb][th][j][q_width]          partial q blocks of kv block j
+ *   full_q_num_blocks / full_q_indices                               fully-live q blocks of kv block j
+ * tb ranges over table_b (1 = broadcast over batch, or B), th over table_h
+ * (1 or Hq).  Partial blocks get the element mask; full blocks skip it.
+ * Blocks absent from both lists are skipped (treated as fully masked).
+ * The forward uses the kv-side tables, the backward both sides.
+ * mask_block_q must be a multiple of the kernel's query tile and
+ * mask_block_kv of its key tile (128 always works).
+ */
+typedef struct fa_params {
+  int32_t abi_version; /* FA_ABI_VERSION */
+  int32_t dtype;       /* enum fa_dtype: q, k, v, o, do, dq, dk, dv */
+  int32_t B, Hq, Hkv, Sq, Skv, D;
+  int32_t block_m, block_n; /* kernel tiles; 0 = library default */
+  float scale;              /* softmax scale; 0 = 1/sqrt(D) */
+  int32_t window_left, window_right;
+  const int32_t *q_doc_ids;  /* (B, Sq) or NULL */
+  const int32_t *kv_doc_ids; /* (B, Skv) or NULL (required iff q_doc_ids) */
+  const float *alibi_slopes; /* (Hq) or NULL */
+  float softcap;             /* 0 = off */
+  int32_t mask_block_q, mask_block_kv;
+  int32_t table_b, table_h;
+  int32_t kv_width, q_width;
+  const int32_t *kv_num_blocks, *kv_indices, *full_kv_num_blocks, *full_kv_indices;
+  const int32_t *q_num_blocks, *q_indices, *full_q_num_blocks, *full_q_indices;
+} fa_params;
+
+/* Forward: o = softmax(mask(score_mod(scale q k^T))) v, lse = logsumexp of the row. */
+int fa_fwd(const fa_params *p, const void *q, const void *k, const void *v, void *o, float *lse,
+           void *stream);
+
+/* Bytes of device scratch fa_bwd needs for these params. */
+size_t fa_bwd_workspace_bytes(const fa_params *p);
+
+/* Backward: gradients of sum(o * dout) w.r.t. q, k, v, given o and lse from fa_fwd.
+ * dk / dv are written (not accumulated); with GQA they sum over the q heads
+ * sharing each kv head. */
+int fa_bwd(const fa_params *p, const void *q, const void *k, const void *v, const void *o,
+           const float *lse, const void *dout, void *dq, void *dk, void *dv, void *workspace,
+           size_t workspace_bytes, void *stream);
+
+const char *fa_strerror(int status);
+int fa_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FLEXATTN_H_ */

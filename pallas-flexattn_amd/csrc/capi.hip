@@ -1,0 +1,252 @@
+// C ABI of libflexattn.so: argument validation, tile-config selection and
+// kernel launches.  See include/flexattn.h for the contract.
+#include <hip/hip_runtime.h>
+
+#include "../../include/flexattn.h"
+#include "bwd.h"
+
+namespace {
+
+using fa::BwdArgs;
+using fa::FwdArgs;
+using fa::Problem;
+
+struct Tiles {
+  int bm, bn;    // forward / dQ: query tile, key tile
+  int bkv, bq;   // dK/dV: key tile, query tile
+};
+
+int default_tiles(const fa_params* p, Tiles* t) {
+  if (p->dtype == FA_DTYPE_BF16) {
+    t->bm = p->block_m ? p->block_m : 128;
+    t->bn = p->block_n ? p->block_n : 64;
+    t->bkv = 128;
+    t->bq = 64;
+    if (!((t->bm == 128 || t->bm == 64) && t->bn == 64)) return FA_ERR_UNSUPPORTED;
+  } else {
+    t->bm = p->block_m ? p->block_m : 128;
+    t->bn = p->block_n ? p->block_n : 32;
+    t->bkv = 128;
+    t->bq = 32;
+    if (!((t->bm == 128 || t->bm == 64) && t->bn == 32)) return FA_ERR_UNSUPPORTED;
+  }
+  return FA_OK;
+}
+
+inline int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+int build_problem(const fa_params* p, const Tiles& t, Problem* pr) {
+  if (!p) return FA_ERR_NULL;
+  if (p->abi_version != FA_ABI_VERSION) return FA_ERR_VERSION;
+  if (p->dtype != FA_DTYPE_BF16 && p->dtype != FA_DTYPE_F32) return FA_ERR_DTYPE;
+  if (p->B < 1 || p->Hq < 1 || p->Hkv < 1 || p->Sq < 1 || p->Skv < 1) return FA_ERR_SHAPE;
+  if (p->Hq % p->Hkv != 0) return FA_ERR_SHAPE;
+  if (p->D != 32 && p->D != 64 && p->D != 128) return FA_ERR_UNSUPPORTED;
+  if (!(p->softcap >= 0.f) || !(p->scale >= 0.f)) return FA_ERR_SHAPE;
+  if ((p->q_doc_ids == nullptr) != (p->kv_doc_ids == nullptr)) return FA_ERR_NULL;
+  Problem& r = *pr;
+  r.B = p->B;
+  r.Hq = p->Hq;
+  r.Hkv = p->Hkv;
+  r.Sq = p->Sq;
+  r.Skv = p->Skv;
+  r.scale = p->scale > 0.f ? p->scale : 1.0f / sqrtf((float)p->D);
+  r.scale_log2 = r.scale * fa::kLog2e;
+  r.win_left = p->window_left < 0 ? -1 : p->window_left;
+  r.win_right = p->window_right < 0 ? -1 : p->window_right;
+  r.q_doc = p->q_doc_ids;
+  r.kv_doc = p->kv_doc_ids;
+  r.alibi = p->alibi_slopes;
+  r.softcap = p->softcap;
+  r.has_mask = (r.win_left >= 0 || r.win_right >= 0 || r.q_doc != nullptr) ? 1 : 0;
+  r.xcd_remap = 1;
+  r.kv_num = p->kv_num_blocks;
+  r.kv_idx = p->kv_indices;
+  r.full_kv_num = p->full_kv_num_blocks;
+  r.full_kv_idx = p->full_kv_indices;
+  r.q_num = p->q_num_blocks;
+  r.q_idx = p->q_indices;
+  r.full_q_num = p->full_q_num_blocks;
+  r.full_q_idx = p->full_q_indices;
+  r.has_tables = (r.kv_num || r.full_kv_num || r.q_num || r.full_q_num) ? 1 : 0;
+  if (r.has_tables) {
+    if ((r.kv_num == nullptr) != (r.kv_idx == nullptr)) return FA_ERR_TABLES;
+    if ((r.full_kv_num == nullptr) != (r.full_kv_idx == nullptr)) return FA_ERR_TABLES;
+    if ((r.q_num == nullptr) != (r.q_idx == nullptr)) return FA_ERR_TABLES;
+    if ((r.full_q_num == nullptr) != (r.full_q_idx == nullptr)) return FA_ERR_TABLES;
+    if (p->mask_block_q < 1 || p->mask_block_kv < 1) return FA_ERR_TABLES;
+    if (p->table_b != 1 && p->table_b != p->B) return FA_ERR_TABLES;
+    if (p->table_h != 1 && p->table_h != p->Hq) return FA_ERR_TABLES;
+    if (p->kv_width < 0 || p->q_width < 0) return FA_ERR_TABLES;
+    r.mblk_q = p->mask_block_q;
+    r.mblk_kv = p->mask_block_kv;
+  } else {
+    r.mblk_q = t.bm;
+    r.mblk_kv = t.bn;
+  }
+  r.tab_b = p->table_b < 1 ? 1 : p->table_b;
+  r.tab_h = p->table_h < 1 ? 1 : p->table_h;
+  r.kv_width = p->kv_width;
+  r.q_width = p->q_width;
+  r.n_qblk = cdiv(p->Sq, r.mblk_q);
+  r.n_kvblk = cdiv(p->Skv, r.mblk_kv);
+  return FA_OK;
+}
+
+int launch_status() { return hipGetLastError() == hipSuccess ? FA_OK : FA_ERR_LAUNCH; }
+
+// ------------------------------------------------------------- forward ----
+template <typename T, int D, int BN, int NW, bool M>
+int run_fwd(const FwdArgs& a, hipStream_t s) {
+  const int grid = a.p.B * a.p.Hq * cdiv(a.p.Sq, 32 * NW);
+  hipLaunchKernelGGL((fa::fwd_kernel<T, D, BN, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
+  return launch_status();
+}
+
+template <typename T, int D, int BN, bool M>
+int fwd_nw(const FwdArgs& a, int bm, hipStream_t s) {
+  return bm == 64 ? run_fwd<T, D, BN, 2, M>(a, s) : run_fwd<T, D, BN, 4, M>(a, s);
+}
+
+template <typename T, int BN, bool M>
+int fwd_d(const FwdArgs& a, int D, int bm, hipStream_t s) {
+  switch (D) {
+    case 32: return fwd_nw<T, 32, BN, M>(a, bm, s);
+    case 64: return fwd_nw<T, 64, BN, M>(a, bm, s);
+    default: return fwd_nw<T, 128, BN, M>(a, bm, s);
+  }
+}
+
+bool has_mods(const Problem& p) { return p.alibi != nullptr || p.softcap > 0.f; }
+
+// ------------------------------------------------------------ backward ----
+template <typename T, int D, int BN, int NW, bool M>
+int run_dq(const BwdArgs& a, hipStream_t s) {
+  const int grid = a.p.B * a.p.Hq * cdiv(a.p.Sq, 32 * NW);
+  hipLaunchKernelGGL((fa::dq_kernel<T, D, BN, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
+  return launch_status();
+}
+
+template <typename T, int D, int BQ, int NW, bool M>
+int run_dkdv(const BwdArgs& a, hipStream_t s) {
+  const int grid = a.p.B * a.p.Hkv * cdiv(a.p.Skv, 32 * NW);
+  hipLaunchKernelGGL((fa::dkdv_kernel<T, D, BQ, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
+  return launch_status();
+}
+
+template <typename T, int D>
+int run_delta(const BwdArgs& a, hipStream_t s) {
+  const int nrows = a.p.B * a.p.Hq * a.p.Sq;
+  const int rpb = 256 / (D * (int)sizeof(T) / 16);
+  hipLaunchKernelGGL((fa::delta_kernel<T, D>), dim3(cdiv(nrows, rpb)), dim3(256), 0, s, a, nrows);
+  return launch_status();
+}
+
+template <typename T, int D, int BN, int BQ, bool M>
+int bwd_all(const BwdArgs& a, int bm, hipStream_t s) {
+  int rc = run_delta<T, D>(a, s);
+  if (rc) return rc;
+  rc = run_dkdv<T, D, BQ, 4, M>(a, s);
+  if (rc) return rc;
+  return bm == 64 ? run_dq<T, D, BN, 2, M>(a, s) : run_dq<T, D, BN, 4, M>(a, s);
+}
+
+template <typename T, int BN, int BQ, bool M>
+int bwd_d(const BwdArgs& a, int D, int bm, hipStream_t s) {
+  switch (D) {
+    case 32: return bwd_all<T, 32, BN, BQ, M>(a, bm, s);
+    case 64: return bwd_all<T, 64, BN, BQ, M>(a, bm, s);
+    default: return bwd_all<T, 128, BN, BQ, M>(a, bm, s);
+  }
+}
+
+size_t delta_bytes(const fa_params* p) {
+  return ((size_t)p->B * p->Hq * p->Sq * sizeof(float) + 255) & ~(size_t)255;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fa_abi_version(void) { return FA_ABI_VERSION; }
+
+const char* fa_strerror(int status) {
+  switch (status) {
+    case FA_OK: return "success";
+    case FA_ERR_NULL: return "a required pointer is null";
+    case FA_ERR_SHAPE: return "invalid or inconsistent sizes";
+    case FA_ERR_DTYPE: return "unknown dtype";
+    case FA_ERR_UNSUPPORTED: return "no kernel for this head dim / tile configuration";
+    case FA_ERR_TABLES: return "block tables inconsistent with the problem sizes";
+    case FA_ERR_WORKSPACE: return "workspace missing or too small";
+    case FA_ERR_LAUNCH: return "HIP kernel launch failed";
+    case FA_ERR_VERSION: return "fa_params.abi_version does not match the library";
+    default: return "unknown status";
+  }
+}
+
+int fa_fwd(const fa_params* p, const void* q, const void* k, const void* v, void* o, float* lse,
+           void* stream) {
+  if (!p) return FA_ERR_NULL;
+  Tiles t;
+  int rc = default_tiles(p, &t);
+  if (rc) return rc;
+  FwdArgs a;
+  rc = build_problem(p, t, &a.p);
+  if (rc) return rc;
+  if (!q || !k || !v || !o || !lse) return FA_ERR_NULL;
+  if (a.p.has_tables && (a.p.mblk_q % t.bm || a.p.mblk_kv % t.bn)) return FA_ERR_TABLES;
+  if (a.p.has_tables && !a.p.kv_num && !a.p.full_kv_num) return FA_ERR_TABLES;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.lse = lse;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool m = has_mods(a.p);
+  if (p->dtype == FA_DTYPE_BF16)
+    return m ? fwd_d<uint16_t, 64, true>(a, p->D, t.bm, s) : fwd_d<uint16_t, 64, false>(a, p->D, t.bm, s);
+  return m ? fwd_d<float, 32, true>(a, p->D, t.bm, s) : fwd_d<float, 32, false>(a, p->D, t.bm, s);
+}
+
+size_t fa_bwd_workspace_bytes(const fa_params* p) {
+  if (!p) return 0;
+  return delta_bytes(p);
+}
+
+int fa_bwd(const fa_params* p, const void* q, const void* k, const void* v, const void* o,
+           const float* lse, const void* dout, void* dq, void* dk, void* dv, void* workspace,
+           size_t workspace_bytes, void* stream) {
+  if (!p) return FA_ERR_NULL;
+  Tiles t;
+  int rc = default_tiles(p, &t);
+  if (rc) return rc;
+  BwdArgs a;
+  rc = build_problem(p, t, &a.p);
+  if (rc) return rc;
+  if (!q || !k || !v || !o || !lse || !dout || !dq || !dk || !dv) return FA_ERR_NULL;
+  if (!workspace || workspace_bytes < delta_bytes(p)) return FA_ERR_WORKSPACE;
+  if (a.p.has_tables) {
+    if (a.p.mblk_q % t.bm || a.p.mblk_kv % t.bn || a.p.mblk_kv % t.bkv || a.p.mblk_q % t.bq)
+      return FA_ERR_TABLES;
+    if (!a.p.kv_num && !a.p.full_kv_num) return FA_ERR_TABLES;
+    if (!a.p.q_num && !a.p.full_q_num) return FA_ERR_TABLES;
+  }
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.lse = lse;
+  a.dout = dout;
+  a.dq = dq;
+  a.dk = dk;
+  a.dv = dv;
+  a.delta = static_cast<float*>(workspace);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool m = has_mods(a.p);
+  if (p->dtype == FA_DTYPE_BF16)
+    return m ? bwd_d<uint16_t, 64, 64, true>(a, p->D, t.bm, s) : bwd_d<uint16_t, 64, 64, false>(a, p->D, t.bm, s);
+  return m ? bwd_d<float, 32, 32, true>(a, p->D, t.bm, s) : bwd_d<float, 32, 32, false>(a, p->D, t.bm, s);
+}
+
+}  // extern "C"

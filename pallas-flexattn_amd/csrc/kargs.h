@@ -1,0 +1,108 @@
+// Kernel argument blocks (passed by value) and the device-side mask /
+// score-modification epilogues shared by the forward and backward kernels.
+#pragma once
+#include "common.h"
+
+namespace fa {
+
+// Everything a kernel needs to know about the attention problem except the
+// tensor pointers.  Built on the host from fa_params.
+struct Problem {
+  int B, Hq, Hkv, Sq, Skv;
+  float scale;       // softmax scale applied to q.k
+  float scale_log2;  // scale * log2(e)
+  // mask: window on delta = q - kv (left/right < 0: unlimited) and documents
+  int win_left, win_right;
+  const int* q_doc;   // (B, Sq) or null
+  const int* kv_doc;  // (B, Skv) or null
+  // score modification: s += alibi[h] * (kv - q); then s = cap * tanh(s / cap)
+  const float* alibi;  // (Hq) or null
+  float softcap;       // <= 0: off
+  // block tables at mask-block granularity (PyTorch BlockMask convention:
+  // kv_* lists the partial blocks, full_kv_* the fully-live ones)
+  const int *kv_num, *kv_idx, *full_kv_num, *full_kv_idx;  // rows = q mask blocks
+  const int *q_num, *q_idx, *full_q_num, *full_q_idx;      // rows = kv mask blocks
+  int tab_b, tab_h;      // 1 or B, 1 or Hq
+  int n_qblk, n_kvblk;   // table rows (q side / kv side)
+  int kv_width, q_width;
+  int mblk_q, mblk_kv;   // mask block sizes
+  int has_tables;        // 0: dense iteration over all blocks
+  int has_mask;          // any window / doc term active
+  int xcd_remap;         // group work of a head onto one XCD
+};
+
+// Window part of the element mask (q, kv inside the sequence bounds).
+__device__ __forceinline__ bool window_ok(const Problem& p, int q, int k) {
+  const int delta = q - k;
+  bool ok = true;
+  if (p.win_left >= 0) ok = ok && (delta <= p.win_left);
+  if (p.win_right >= 0) ok = ok && (-delta <= p.win_right);
+  return ok;
+}
+
+// Full element mask given the two document ids (ignored without documents).
+__device__ __forceinline__ bool mask_ok(const Problem& p, int q, int k, int qdoc, int kdoc) {
+  return window_ok(p, q, k) && (p.q_doc == nullptr || qdoc == kdoc);
+}
+
+__device__ __forceinline__ int kv_doc_of(const Problem& p, int b, int k) {
+  return p.q_doc ? p.kv_doc[(size_t)b * p.Skv + k] : 0;
+}
+__device__ __forceinline__ int q_doc_of(const Problem& p, int b, int q) {
+  return p.q_doc ? p.q_doc[(size_t)b * p.Sq + q] : 0;
+}
+
+// Score epilogue: raw q.k -> log2-domain logit t = s * log2(e), where
+// s = softcap(alibi(scale * raw)).  Also returns d s / d(scale*raw) for the
+// backward (1 without soft-cap).
+template <bool kMods>
+__device__ __forceinline__ float score_t(const Problem& p, float raw, float slope, int q, int k,
+                                         float* dsdx) {
+  if constexpr (!kMods) {
+    if (dsdx) *dsdx = 1.0f;
+    return raw * p.scale_log2;
+  } else {
+    float s = raw * p.scale;
+    if (p.alibi) s += slope * (float)(k - q);
+    if (p.softcap > 0.f) {
+      const float th = tanh_fast(s * (1.0f / p.softcap));
+      s = p.softcap * th;
+      if (dsdx) *dsdx = 1.0f - th * th;
+    } else if (dsdx) {
+      *dsdx = 1.0f;
+    }
+    return s * kLog2e;
+  }
+}
+
+// Tile start used for out-of-range table entries: beyond any sequence, so the
+// tile is skipped and its loads are predicated off.
+constexpr int kPastEnd = 0x40000000;
+
+__device__ __forceinline__ int clamp_count(int n, int width) { return n < 0 ? 0 : (n > width ? width : n); }
+
+// Row of the block tables for (b, h, row).
+__device__ __forceinline__ int tab_row(const Problem& p, int b, int h, int row, int nrows) {
+  const int tb = p.tab_b == 1 ? 0 : b;
+  const int th = p.tab_h == 1 ? 0 : h;
+  return (tb * p.tab_h + th) * nrows + row;
+}
+
+// Work-item order: blockIdx.x is dispatched round-robin over the 8 XCDs.  With
+// remapping, XCD x processes heads [x*H/8, (x+1)*H/8) one after another, each
+// head's tiles in reverse order (longest causal rows first), so the K/V (or
+// Q/dO) of a head stay in that XCD's L2 while its tiles run.
+__device__ __forceinline__ void work_item(int bid, int nheads, int ntiles, bool remap, int* head,
+                                          int* tile) {
+  if (remap && (nheads % 8) == 0) {
+    const int xcd = bid & 7, slot = bid >> 3;
+    const int hpx = nheads >> 3;
+    *head = xcd * hpx + slot / ntiles;
+    *tile = ntiles - 1 - (slot % ntiles);
+  } else {
+    *head = bid / ntiles;
+    *tile = ntiles - 1 - (bid % ntiles);
+  }
+}
+
+}  // namespace fa

@@ -1,0 +1,343 @@
+"""FlexAttention on MI355X: host side of ``flash_attn.py`` of the reference.
+
+Input shapes: q (B, Hq, T, D); k, v (B, Hkv, T, D) with Hq % Hkv == 0
+(grouped-query attention; the reference requires Hq == Hkv).  Tensors are
+torch tensors on the GPU (bf16 or fp32); the kernels run through the C ABI of
+libflexattn.so on the current torch stream.
+
+Entry points keep the reference's signatures:
+
+* :func:`flash_attention` (``flash_attn.py:464-504``): differentiable output
+  (a ``torch.autograd.Function`` replaces ``jax.custom_vjp``; the residuals are
+  ``(q, k, v, o, lse)`` as at ``:487``, with the LSE kept in fp32),
+* :func:`flash_attention_fwd` (``:111-165``) -> ``(o, lse)``, LSE returned in q's
+  dtype as the reference does (``:144``),
+* :func:`flash_attention_bwd` (``:410-461``) -> ``(dq, dk, dv)``,
+* :func:`mha_reference` (``:33-56``): materialised attention,
+
+plus the FlexAttention front door :func:`flex_attention` (``score_mod``,
+``block_mask``, ``scale``, ``enable_gqa``, ``return_lse``, ``kernel_options``).
+
+``interpret=True`` selected the Pallas interpreter on the host in the
+reference; this build has no host execution path and raises.
+"""
+import math
+from typing import Optional, Tuple
+
+import numpy as np
+
+from . import _lib
+from .block_mask import BlockMask, _finish
+from .kernel_tuner import (DEFAULT_BLOCK_C, DEFAULT_BLOCK_R, DEFAULT_NUM_STAGES, DEFAULT_NUM_WARPS,
+                           kernel_tiles, tuned_tiles)
+from .mask_mod import MaskSpec, MaskMod
+from .score_mod import ScoreSpec
+
+# Granularity of the block tables built internally: a multiple of every
+# kernel tile (64/128 queries, 32/64 keys, 128-key dK/dV tiles).
+TABLE_BLOCK = 128
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def _dtype_code(t):
+    torch = _torch()
+    if t.dtype == torch.bfloat16:
+        return _lib.DTYPE_BF16, "bf16"
+    if t.dtype == torch.float32:
+        return _lib.DTYPE_F32, "fp32"
+    raise TypeError(f"unsupported dtype {t.dtype}: the MI355X kernels take bfloat16 or float32")
+
+
+def _check_interpret(interpret):
+    if interpret:
+        raise NotImplementedError(
+            "interpret=True ran the Pallas interpreter on the host; this MI355X build only executes its "
+            "HIP kernels on the GPU. Pass GPU tensors with interpret=False (mha_reference gives a "
+            "materialised reference result).")
+
+
+def _check_inputs(q, k, v):
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must be (B, H, T, D)")
+    if not (q.is_cuda and k.is_cuda and v.is_cuda):
+        raise ValueError("q, k, v must be GPU tensors")
+    if q.dtype != k.dtype or q.dtype != v.dtype:
+        raise TypeError("q, k, v must share a dtype")
+    B, Hq, Sq, D = q.shape
+    if k.shape[0] != B or v.shape[0] != B or k.shape[3] != D or v.shape[3] != D:
+        raise ValueError("batch / head-dim mismatch between q, k, v")
+    if k.shape[1] != v.shape[1] or k.shape[2] != v.shape[2]:
+        raise ValueError("k and v must have the same shape")
+    if Hq % k.shape[1] != 0:
+        raise ValueError("number of q heads must be a multiple of the number of kv heads")
+
+
+class _Plan:
+    """Everything the C ABI needs besides the tensors: an fa_params struct
+    plus the device arrays its pointers refer to (kept alive here)."""
+
+    def __init__(self, q, k, mask: Optional[MaskSpec], score: Optional[ScoreSpec], scale: Optional[float],
+                 block_mask: Optional[BlockMask], tiles: Tuple[int, int]):
+        torch = _torch()
+        B, Hq, Sq, D = q.shape
+        Hkv, Skv = k.shape[1], k.shape[2]
+        code, dname = _dtype_code(q)
+        p = _lib.FaParams()
+        p.abi_version = _lib.ABI_VERSION
+        p.dtype = code
+        p.B, p.Hq, p.Hkv, p.Sq, p.Skv, p.D = B, Hq, Hkv, Sq, Skv, D
+        p.block_m, p.block_n = tiles
+        p.scale = 0.0 if scale is None else float(scale)
+        p.window_left = p.window_right = -1
+        self.keep = []
+        dev = q.device
+        if mask is not None:
+            p.window_left, p.window_right = mask.left, mask.right
+            if mask.doc_ids is not None:
+                docs = mask.doc_ids
+                if docs.shape[1] < max(Sq, Skv):
+                    raise ValueError("document ids are shorter than the sequence")
+                if docs.shape[0] not in (1, B):
+                    raise ValueError("document ids must have 1 or B rows")
+                dq_ = np.array(np.broadcast_to(docs[:, :Sq], (B, Sq)), dtype=np.int32)
+                dk_ = np.array(np.broadcast_to(docs[:, :Skv], (B, Skv)), dtype=np.int32)
+                tq = torch.from_numpy(dq_).to(dev)
+                tk = torch.from_numpy(dk_).to(dev)
+                self.keep += [tq, tk]
+                p.q_doc_ids, p.kv_doc_ids = tq.data_ptr(), tk.data_ptr()
+        if score is not None:
+            if score.alibi is not None:
+                if score.alibi.shape[0] != Hq:
+                    raise ValueError(f"ALiBi needs one slope per q head ({Hq}), got {score.alibi.shape[0]}")
+                ts = torch.from_numpy(score.alibi).to(dev)
+                self.keep.append(ts)
+                p.alibi_slopes = ts.data_ptr()
+            p.softcap = score.softcap
+        if block_mask is not None:
+            if block_mask.q_len != Sq or block_mask.kv_len != Skv:
+                raise ValueError(f"block mask built for ({block_mask.q_len}, {block_mask.kv_len}), "
+                                 f"inputs are ({Sq}, {Skv})")
+            bs = block_mask.block_size
+            if bs % tiles[0] or bs % tiles[1] or bs % 128:
+                raise ValueError(f"block_size {bs} must be a multiple of 128 and of the kernel tiles {tiles}")
+            tb, th = block_mask.table_shape
+            if tb not in (1, B) or th not in (1, Hq):
+                raise ValueError("block mask tables do not broadcast over (B, H)")
+            t = block_mask.device_tables(dev)
+            p.mask_block_q = p.mask_block_kv = bs
+            p.table_b, p.table_h = tb, th
+            p.kv_width = t["kv_indices"].shape[-1]
+            p.q_width = t["q_indices"].shape[-1]
+            for name in t:
+                setattr(p, name, t[name].data_ptr())
+        self.params = p
+        self.dname = dname
+
+    def ptr(self):
+        import ctypes
+        return ctypes.byref(self.params)
+
+
+_MASK_CACHE = {}
+
+
+def _internal_block_mask(mask: MaskSpec, B: int, Sq: int, Skv: int) -> BlockMask:
+    key = (mask.key(), B, Sq, Skv)
+    bm = _MASK_CACHE.get(key)
+    if bm is None:
+        bm = _finish(None, None, mask, B, 1, Sq, Skv, TABLE_BLOCK)
+        if len(_MASK_CACHE) > 64:
+            _MASK_CACHE.clear()
+        _MASK_CACHE[key] = bm
+    return bm
+
+
+def _as_mask_spec(mask_mod) -> Optional[MaskSpec]:
+    if mask_mod is None:
+        return None
+    if isinstance(mask_mod, MaskSpec):
+        return mask_mod
+    raise NotImplementedError(
+        "the MI355X kernels evaluate mask mods as fused epilogues: use causal_mask, bidirectional_mask, "
+        "sliding_window_mask, document_mask or and_masks of them (arbitrary callables work with "
+        "create_block_mask and mha_reference only)")
+
+
+def _as_score_spec(score_mod) -> Optional[ScoreSpec]:
+    if score_mod is None:
+        return None
+    if isinstance(score_mod, ScoreSpec):
+        return None if (score_mod.alibi is None and score_mod.softcap == 0) else score_mod
+    raise NotImplementedError(
+        "the MI355X kernels support the fused score mods alibi_score_mod, softcap_score_mod and their "
+        "composition; arbitrary callables are not lowered")
+
+
+def _stream():
+    return _torch().cuda.current_stream().cuda_stream
+
+
+def _dense16(t):
+    """Contiguous with a 16-byte aligned base (the kernels use 16-byte loads)."""
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def _fwd_core(q, k, v, mask, score, scale, block_mask, tiles):
+    torch = _torch()
+    _check_inputs(q, k, v)
+    q, k, v = _dense16(q), _dense16(k), _dense16(v)
+    if block_mask is None and mask is not None and not mask.is_trivial:
+        block_mask = _internal_block_mask(mask, q.shape[0], q.shape[2], k.shape[2])
+    plan = _Plan(q, k, mask, score, scale, block_mask, tiles)
+    o = torch.empty_like(q)
+    lse = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
+    lib = _lib.load()
+    _lib.check(lib.fa_fwd(plan.ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                          _stream()))
+    return o, lse
+
+
+def _bwd_core(q, k, v, o, lse, do, mask, score, scale, block_mask, tiles):
+    torch = _torch()
+    _check_inputs(q, k, v)
+    if do.dtype != q.dtype:
+        do = do.to(q.dtype)
+    q, k, v, o, do = (_dense16(t) for t in (q, k, v, o, do))
+    lse = lse.to(torch.float32).contiguous()
+    if o.shape != q.shape or do.shape != q.shape or lse.shape != q.shape[:3]:
+        raise ValueError("o / do / lse shapes do not match q")
+    if block_mask is None and mask is not None and not mask.is_trivial:
+        block_mask = _internal_block_mask(mask, q.shape[0], q.shape[2], k.shape[2])
+    plan = _Plan(q, k, mask, score, scale, block_mask, tiles)
+    lib = _lib.load()
+    ws_bytes = lib.fa_bwd_workspace_bytes(plan.ptr())
+    ws = torch.empty(max(ws_bytes, 256), device=q.device, dtype=torch.uint8)
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    _lib.check(lib.fa_bwd(plan.ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                          do.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(),
+                          ws.numel(), _stream()))
+    return dq, dk, dv
+
+
+def _ref_tiles(q, block_r, block_c):
+    _, dname = _dtype_code(q)
+    return kernel_tiles(block_r, block_c, dname)
+
+
+# ------------------------------------------------------------ public API ----
+def mha_reference(q, k, v, mask_mod: Optional[MaskMod] = None):
+    """Materialised attention (``flash_attn.py:33-56``): ``softmax(where(mask,
+    q k^T / sqrt(d), -inf)) v`` computed in the input dtype with torch ops.
+    Accepts any mask mod callable (and GQA inputs)."""
+    torch = _torch()
+    d = q.shape[-1]
+    g = q.shape[1] // k.shape[1]
+    if g > 1:
+        k = k.repeat_interleave(g, dim=1)
+        v = v.repeat_interleave(g, dim=1)
+    logits = torch.matmul(q, k.transpose(-1, -2).contiguous()) / math.sqrt(d)
+    T, S = q.shape[2], k.shape[2]
+    if mask_mod is not None:
+        q_idx = torch.arange(T, device=q.device)[:, None]
+        kv_idx = torch.arange(S, device=q.device)[None, :]
+        mask = mask_mod(q_idx, kv_idx)
+        logits = torch.where(mask, logits, torch.tensor(float("-inf"), dtype=logits.dtype, device=q.device))
+    probs = torch.softmax(logits, dim=-1)
+    return torch.matmul(probs, v.contiguous())
+
+
+def flash_attention_fwd(q, k, v, mask_mod: Optional[MaskMod] = None, block_r: int = DEFAULT_BLOCK_R,
+                        block_c: int = DEFAULT_BLOCK_C, num_warps: int = DEFAULT_NUM_WARPS,
+                        num_stages: int = DEFAULT_NUM_STAGES, interpret: bool = False):
+    """Forward pass -> (o, logsumexp) with logsumexp in q's dtype (``flash_attn.py:111-165``)."""
+    _check_interpret(interpret)
+    o, lse = _fwd_core(q, k, v, _as_mask_spec(mask_mod), None, None, None, _ref_tiles(q, block_r, block_c))
+    return o, lse.to(q.dtype)
+
+
+def flash_attention_bwd(q, k, v, o, logsumexp, do, mask_mod: Optional[MaskMod] = None,
+                        block_r: int = DEFAULT_BLOCK_R, block_c: int = DEFAULT_BLOCK_C,
+                        num_warps: int = DEFAULT_NUM_WARPS, num_stages: int = DEFAULT_NUM_STAGES,
+                        interpret: bool = False):
+    """Backward pass -> (dq, dk, dv) (``flash_attn.py:410-461``).  ``logsumexp``
+    may be in q's dtype (as returned by :func:`flash_attention_fwd`) or fp32."""
+    _check_interpret(interpret)
+    return _bwd_core(q, k, v, o, logsumexp, do, _as_mask_spec(mask_mod), None, None, None,
+                     _ref_tiles(q, block_r, block_c))
+
+
+class _FlexFn:
+    """torch.autograd.Function wrapper (created lazily so that importing the
+    package does not require torch)."""
+    fn = None
+
+    @classmethod
+    def get(cls):
+        if cls.fn is None:
+            torch = _torch()
+
+            class FlexAttnFunction(torch.autograd.Function):
+                @staticmethod
+                def forward(ctx, q, k, v, cfg):
+                    o, lse = _fwd_core(q, k, v, *cfg)
+                    ctx.save_for_backward(q, k, v, o, lse)
+                    ctx.cfg = cfg
+                    ctx.mark_non_differentiable(lse)
+                    return o, lse
+
+                @staticmethod
+                def backward(ctx, do, dlse):
+                    q, k, v, o, lse = ctx.saved_tensors
+                    dq, dk, dv = _bwd_core(q, k, v, o, lse, do, *ctx.cfg)
+                    return dq, dk, dv, None
+
+            cls.fn = FlexAttnFunction
+        return cls.fn
+
+
+def flash_attention(q, k, v, mask_mod: Optional[MaskMod] = None, block_r: int = DEFAULT_BLOCK_R,
+                    block_c: int = DEFAULT_BLOCK_C, num_warps: int = DEFAULT_NUM_WARPS,
+                    num_stages: int = DEFAULT_NUM_STAGES, interpret: bool = False):
+    """Flash attention with a custom backward (``flash_attn.py:464-504``)."""
+    _check_interpret(interpret)
+    cfg = (_as_mask_spec(mask_mod), None, None, None, _ref_tiles(q, block_r, block_c))
+    o, _ = _FlexFn.get().apply(q, k, v, cfg)
+    return o
+
+
+def flex_attention(query, key, value, score_mod: Optional[ScoreSpec] = None,
+                   block_mask: Optional[BlockMask] = None, scale: Optional[float] = None,
+                   enable_gqa: bool = False, return_lse: bool = False, kernel_options: Optional[dict] = None):
+    """FlexAttention: ``softmax(mask(score_mod(scale * q k^T))) v`` over the
+    blocks of ``block_mask`` (all blocks when None).  Differentiable.
+
+    ``kernel_options`` may set ``BLOCK_M`` / ``BLOCK_N``; otherwise a tuned
+    table entry or the defaults (bf16: 128 x 64, fp32: 128 x 32) are used."""
+    if query.shape[1] != key.shape[1] and not enable_gqa:
+        raise ValueError("query and key head counts differ: pass enable_gqa=True for grouped-query attention")
+    mask = None
+    if block_mask is not None:
+        mask = _as_mask_spec(block_mask.mask_mod) if block_mask.mask_mod is not None else None
+        if not block_mask.has_tables:
+            raise ValueError("block_mask has no kernel tables (build it with create_block_mask)")
+        if block_mask.block_size % TABLE_BLOCK and mask is not None:
+            # the dK/dV kernel walks 128-key tiles: re-derive the exact tables at 128
+            block_mask = _internal_block_mask(mask, query.shape[0], query.shape[2], key.shape[2])
+    _, dname = _dtype_code(query)
+    opts = kernel_options or {}
+    tiles = None
+    if "BLOCK_M" in opts or "BLOCK_N" in opts:
+        tiles = (int(opts.get("BLOCK_M", 128)), int(opts.get("BLOCK_N", 64 if dname == "bf16" else 32)))
+    else:
+        tiles = tuned_tiles(query.shape[2], query.shape[3], dname, block_mask is not None) or \
+            (128, 64 if dname == "bf16" else 32)
+    cfg = (mask, _as_score_spec(score_mod), scale, block_mask, tiles)
+    o, lse = _FlexFn.get().apply(query, key, value, cfg)
+    return (o, lse) if return_lse else o

@@ -1,0 +1,212 @@
+"""Kernel tuner (``kernel_tuner.py`` of the reference).
+
+``get_optimal_params`` / ``get_kernel_config`` / ``print_kernel_config`` keep
+the reference's static table and signatures (``kernel_tuner.py:11-148``).
+Their four numbers are the reference's Triton knobs; :func:`kernel_tiles`
+maps them onto the MI355X kernels' tile choices:
+
+* ``block_r``  -> query tile BLOCK_M of the forward / dQ kernels (64 or 128;
+  each wave owns 32 query rows, so BLOCK_M / 32 waves per workgroup),
+* ``block_c``  -> key tile BLOCK_N (bf16: 64, fp32: 32 — the tiles the LDS
+  layout is built for),
+* ``num_warps``/``num_stages`` are accepted and recorded; wave count follows
+  BLOCK_M and the kernels double-buffer through registers.
+
+:func:`tune` measures the available instantiations on the current GPU and
+stores the winners in a JSON table that ``flex_attention`` consults.
+"""
+import functools
+import json
+import os
+from typing import Dict, Optional, Tuple
+
+DEFAULT_BLOCK_R = 64
+DEFAULT_BLOCK_C = 64
+DEFAULT_NUM_WARPS = 4
+DEFAULT_NUM_STAGES = 3
+
+
+@functools.lru_cache(maxsize=128)
+def get_optimal_params(
+    seq_len: int,
+    head_dim: int = 64,
+    use_block_sparsity: bool = False,
+) -> Tuple[int, int, int, int]:
+    """(block_r, block_c, num_warps, num_stages) for a sequence length
+    (the reference's thresholds, ``kernel_tuner.py:28-63``)."""
+    if seq_len <= 256:
+        block_r, block_c, num_warps, num_stages = 32, 32, 4, 2
+    elif seq_len <= 512:
+        block_r, block_c, num_warps, num_stages = 64, 64, 4, 3
+    elif seq_len <= 2048:
+        block_r, block_c, num_warps, num_stages = 128, 64, 4, 3
+    elif seq_len <= 4096:
+        block_r, block_c, num_warps, num_stages = 128, 128, 8, 4
+    else:
+        block_r, block_c, num_warps, num_stages = 128, 128, 8, 5
+
+    if head_dim > 128:
+        block_r = min(block_r, 64)
+        block_c = min(block_c, 64)
+        num_stages = min(num_stages, 3)
+    elif head_dim <= 32:
+        num_stages = max(num_stages, 4)
+
+    if use_block_sparsity:
+        block_r = min(block_r, 64)
+        block_c = min(block_c, 64)
+
+    return block_r, block_c, num_warps, num_stages
+
+
+def get_kernel_config(
+    batch_size: int,
+    num_heads: int,
+    seq_len: int,
+    head_dim: int,
+    mask_type: Optional[str] = None,
+) -> Dict[str, int]:
+    """Configuration dictionary (``kernel_tuner.py:68-101``)."""
+    use_block_sparsity = mask_type in ('causal', 'sliding_window')
+    block_r, block_c, num_warps, num_stages = get_optimal_params(seq_len, head_dim, use_block_sparsity)
+    return {
+        'batch_size': batch_size,
+        'num_heads': num_heads,
+        'seq_len': seq_len,
+        'head_dim': head_dim,
+        'block_r': block_r,
+        'block_c': block_c,
+        'num_warps': num_warps,
+        'num_stages': num_stages,
+    }
+
+
+def print_kernel_config(
+    batch_size: int,
+    num_heads: int,
+    seq_len: int,
+    head_dim: int,
+    mask_type: Optional[str] = None,
+):
+    """Print the configuration (``kernel_tuner.py:104-148``) plus the MI355X tiles it maps to."""
+    config = get_kernel_config(batch_size, num_heads, seq_len, head_dim, mask_type)
+    bm, bn = kernel_tiles(config['block_r'], config['block_c'], "bf16")
+    print("=" * 70)
+    print("MI355X FlexAttention Kernel Configuration")
+    print("=" * 70)
+    print("Input Configuration:")
+    print(f"  Batch size (B):   {config['batch_size']}")
+    print(f"  Num heads (H):    {config['num_heads']}")
+    print(f"  Seq length (T):   {config['seq_len']}")
+    print(f"  Head dim (D):     {config['head_dim']}")
+    if mask_type:
+        print(f"  Mask type:        {mask_type}")
+    print()
+    print("Kernel Parameters:")
+    print(f"  BLOCK_R (block_r):      {config['block_r']}")
+    print(f"  BLOCK_C (block_c):      {config['block_c']}")
+    print(f"  NUM_WARPS:              {config['num_warps']}")
+    print(f"  NUM_STAGES:             {config['num_stages']}")
+    print(f"  gfx950 tiles (bf16):    BLOCK_M={bm} ({bm // 32} waves), BLOCK_N={bn}")
+    print()
+    print("Usage:")
+    print("  from pallas_flexattn import flash_attention")
+    print("  out = flash_attention(")
+    print("      q, k, v,")
+    print(f"      block_r={config['block_r']},")
+    print(f"      block_c={config['block_c']},")
+    print(f"      num_warps={config['num_warps']},")
+    print(f"      num_stages={config['num_stages']},")
+    print("  )")
+    print("=" * 70)
+
+
+# -- MI355X tile selection ----------------------------------------------------
+SUPPORTED_BLOCK_M = (64, 128)
+SUPPORTED_BLOCK_N = {"bf16": (64,), "fp32": (32,)}
+
+
+def kernel_tiles(block_r: int, block_c: int, dtype: str) -> Tuple[int, int]:
+    """Map the reference's (block_r, block_c) onto an instantiated
+    (BLOCK_M, BLOCK_N): the largest supported BLOCK_M not above
+    max(block_r, 64), and the dtype's key tile."""
+    bm = 128 if block_r >= 128 else 64
+    bn = SUPPORTED_BLOCK_N[dtype][0]
+    return bm, bn
+
+
+TUNE_TABLE = os.environ.get(
+    "FLEXATTN_TUNE_TABLE", os.path.join(os.path.dirname(os.path.abspath(__file__)), "tune_table.json"))
+
+
+def load_tune_table(path: str = TUNE_TABLE) -> Dict[str, Dict[str, int]]:
+    if not os.path.exists(path):
+        return {}
+    with open(path) as f:
+        return json.load(f)
+
+
+def tuned_tiles(seq_len: int, head_dim: int, dtype: str, sparse: bool) -> Optional[Tuple[int, int]]:
+    """Tiles recorded by :func:`tune` for this shape class, if any."""
+    table = load_tune_table()
+    key = f"{dtype}/D{head_dim}/S{seq_len}/{'sparse' if sparse else 'dense'}"
+    e = table.get(key)
+    return (e["block_m"], e["block_n"]) if e else None
+
+
+def tune(batch: int = 4, heads: int = 32, seq_len: int = 4096, head_dim: int = 128, causal: bool = True,
+         dtype: str = "bf16", iters: int = 10, path: str = TUNE_TABLE) -> Dict[str, int]:
+    """Time every instantiated BLOCK_M for this shape on the current GPU
+    (fwd + bwd with hipEvents) and record the fastest in the JSON table."""
+    import torch
+    from .flash_attn import flex_attention
+    from .block_mask import create_block_mask
+    from .mask_mod import causal_mask, bidirectional_mask
+    dt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(0)
+    q, k, v, do = (torch.randn(batch, heads, seq_len, head_dim, device=dev, dtype=dt, generator=g) for _ in range(4))
+    bm_mask = create_block_mask(causal_mask if causal else bidirectional_mask, 1, 1, seq_len, seq_len, 128)
+    results = {}
+    for bm in SUPPORTED_BLOCK_M:
+        for bn in SUPPORTED_BLOCK_N[dtype]:
+            opts = {"BLOCK_M": bm, "BLOCK_N": bn}
+            qq, kk, vv = (t.detach().requires_grad_() for t in (q, k, v))
+            for _ in range(2):
+                o = flex_attention(qq, kk, vv, block_mask=bm_mask, kernel_options=opts)
+                o.backward(do)
+            torch.cuda.synchronize()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            for _ in range(iters):
+                o = flex_attention(qq, kk, vv, block_mask=bm_mask, kernel_options=opts)
+                o.backward(do)
+            e.record()
+            torch.cuda.synchronize()
+            results[(bm, bn)] = s.elapsed_time(e) / iters
+    (bm, bn), ms = min(results.items(), key=lambda kv: kv[1])
+    table = load_tune_table(path)
+    key = f"{dtype}/D{head_dim}/S{seq_len}/{'sparse' if causal else 'dense'}"
+    table[key] = {"block_m": bm, "block_n": bn, "ms_fwd_bwd": ms,
+                  "candidates": {f"{a}x{b}": t for (a, b), t in results.items()}}
+    with open(path, "w") as f:
+        json.dump(table, f, indent=1, sort_keys=True)
+    return table[key]
+
+
+if __name__ == "__main__":
+    import argparse
+
+    parser = argparse.ArgumentParser(description="Kernel parameters for MI355X FlexAttention")
+    parser.add_argument("--batch-size", type=int, default=2)
+    parser.add_argument("--num-heads", type=int, default=8)
+    parser.add_argument("--seq-len", type=int, default=2048)
+    parser.add_argument("--head-dim", type=int, default=64)
+    parser.add_argument("--mask-type", type=str, default=None,
+                        choices=['causal', 'sliding_window', 'bidirectional'])
+    parser.add_argument("--tune", action="store_true", help="measure tiles on this GPU and record them")
+    args = parser.parse_args()
+    if args.tune:
+        print(tune(args.batch_size, args.num_heads, args.seq_len, args.head_dim, args.mask_type == "causal"))
+    else:
+        print_kernel_config(args.batch_size, args.num_heads, args.seq_len, args.head_dim, args.mask_type)

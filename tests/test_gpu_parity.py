@@ -1,0 +1,129 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the float64 oracle.
+
+Tolerances: bf16 atol = rtol = 2e-2 on O, dQ, dK, dV (and LSE); fp32 atol =
+rtol = 1e-5.  Inputs are seeded numpy normals (bf16 values rounded RNE)."""
+import zlib
+
+import numpy as np
+import pytest
+
+from _cases import (BF16_TOL, FP32_TOL, assert_close, inputs, oracle_fwd_bwd, oracle_mask, to_np,
+                    to_torch)
+
+pytestmark = pytest.mark.gpu
+
+
+def _pf():
+    import pallas_flexattn as pf
+    return pf
+
+
+def _doc_lengths(rng, S):
+    out, tot = [], 0
+    while tot < S:
+        n = int(rng.integers(24, 160))
+        n = min(n, S - tot)
+        out.append(n)
+        tot += n
+    return out
+
+
+CASES = [
+    # name, dtype, B, Hq, Hkv, S, D, mask, extras
+    ("causal-bf16-d128", "bf16", 2, 4, 4, 256, 128, ("causal",), {}),
+    ("causal-fp32-d64", "fp32", 1, 4, 4, 256, 64, ("causal",), {}),
+    ("dense-bf16-d64-ragged", "bf16", 2, 2, 2, 192, 64, ("none",), {}),
+    ("window-bf16-d128", "bf16", 1, 2, 2, 512, 128, ("window", 100, 0), {}),
+    ("window-sym-bf16-d64", "bf16", 1, 2, 2, 384, 64, ("window", 32, 32), {}),
+    ("doc-causal-bf16-d128", "bf16", 2, 2, 2, 512, 128, ("doc",), {}),
+    ("gqa-alibi-softcap-bf16", "bf16", 1, 8, 2, 256, 128, ("causal",), {"alibi": True, "softcap": 50.0}),
+    ("ragged-causal-bf16-d128", "bf16", 1, 2, 2, 300, 128, ("causal",), {}),
+    ("dense-fp32-d32", "fp32", 1, 2, 2, 128, 32, ("none",), {}),
+    ("causal-bf16-d32", "bf16", 1, 2, 2, 256, 32, ("causal",), {}),
+    ("softcap-fp32-d128", "fp32", 1, 2, 1, 160, 128, ("causal",), {"softcap": 20.0, "alibi": True}),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_flex_attention_fwd_bwd(case):
+    import torch
+    pf = _pf()
+    name, dtype, B, Hq, Hkv, S, D, mspec, extras = case
+    print(f"[gpu parity] {name}", flush=True)
+    q, k, v, do = inputs(zlib.crc32(name.encode()) % 1000, B, Hq, Hkv, S, S, D, dtype)
+    kind = mspec[0]
+    doc_ids = None
+    if kind == "causal":
+        mm = pf.causal_mask
+    elif kind == "window":
+        mm = pf.sliding_window_mask(mspec[1], mspec[2])
+    elif kind == "doc":
+        rng = np.random.default_rng(7)
+        lens = [_doc_lengths(rng, S) for _ in range(B)]
+        dm = pf.document_mask(lens)
+        doc_ids = dm.doc_ids
+        mm = pf.and_masks(dm, pf.causal_mask)
+    else:
+        mm = None
+    omask = oracle_mask("causal" if kind == "doc" else kind, S, S, B,
+                        *(mspec[1:] if kind == "window" else ()), doc_ids=doc_ids)
+    alibi = pf.alibi_slopes(Hq) if extras.get("alibi") else None
+    softcap = extras.get("softcap")
+    score = None
+    if alibi is not None or softcap:
+        parts = []
+        if alibi is not None:
+            parts.append(pf.alibi_score_mod(alibi))
+        if softcap:
+            parts.append(pf.softcap_score_mod(softcap))
+        score = pf.compose_score_mods(*parts)
+    bm = pf.create_block_mask(mm, B, Hq, S, S, 128) if mm is not None else None
+
+    tq, tk, tv = (to_torch(x, dtype).requires_grad_() for x in (q, k, v))
+    tdo = to_torch(do, dtype)
+    o, lse = pf.flex_attention(tq, tk, tv, score_mod=score, block_mask=bm, enable_gqa=Hq != Hkv, return_lse=True)
+    o.backward(tdo)
+    torch.cuda.synchronize()
+
+    want_o, want_lse, (wdq, wdk, wdv) = oracle_fwd_bwd(q, k, v, do, omask, alibi=alibi, softcap=softcap)
+    tol = BF16_TOL if dtype == "bf16" else FP32_TOL
+    assert_close(f"{name} O", to_np(o), want_o, tol)
+    assert_close(f"{name} LSE", to_np(lse), want_lse, tol)
+    assert_close(f"{name} dQ", to_np(tq.grad), wdq, tol)
+    assert_close(f"{name} dK", to_np(tk.grad), wdk, tol)
+    assert_close(f"{name} dV", to_np(tv.grad), wdv, tol)
+
+
+def test_reference_api_fwd_bwd_causal_bf16():
+    """flash_attention_fwd / flash_attention_bwd with the reference's signatures."""
+    pf = _pf()
+    import torch
+    B, H, S, D = 2, 4, 256, 128
+    q, k, v, do = inputs(11, B, H, H, S, S, D, "bf16", scale=0.5)
+    tq, tk, tv, tdo = (to_torch(x, "bf16") for x in (q, k, v, do))
+    o, lse = pf.flash_attention_fwd(tq, tk, tv, mask_mod=pf.causal_mask, block_r=128, block_c=64)
+    assert lse.dtype == torch.bfloat16  # LSE in q's dtype, as the reference stores it
+    dq, dk, dv = pf.flash_attention_bwd(tq, tk, tv, o, lse, tdo, mask_mod=pf.causal_mask)
+    mask = oracle_mask("causal", S, S)
+    wo, wl, (wdq, wdk, wdv) = oracle_fwd_bwd(q, k, v, do, mask)
+    assert_close("O", to_np(o), wo, BF16_TOL)
+    assert_close("LSE", to_np(lse), wl, BF16_TOL)
+    # the bf16-rounded LSE (a reference quirk) perturbs P by up to ~1.5%
+    assert_close("dQ", to_np(dq), wdq, dict(atol=3e-2, rtol=3e-2))
+    assert_close("dK", to_np(dk), wdk, dict(atol=3e-2, rtol=3e-2))
+    assert_close("dV", to_np(dv), wdv, dict(atol=3e-2, rtol=3e-2))
+
+
+def test_flash_attention_autograd_fp32_block64():
+    """flash_attention (custom backward) at the fp32 C1 shape: B1 H4 S256 D64, causal, block 64."""
+    pf = _pf()
+    B, H, S, D = 1, 4, 256, 64
+    q, k, v, do = inputs(0, B, H, H, S, S, D, "fp32")
+    tq, tk, tv = (to_torch(x, "fp32").requires_grad_() for x in (q, k, v))
+    o = pf.flash_attention(tq, tk, tv, mask_mod=pf.causal_mask, block_r=64, block_c=64)
+    o.backward(to_torch(do, "fp32"))
+    wo, _, (wdq, wdk, wdv) = oracle_fwd_bwd(q, k, v, do, oracle_mask("causal", S, S))
+    assert_close("O", to_np(o), wo, FP32_TOL)
+    assert_close("dQ", to_np(tq.grad), wdq, FP32_TOL)
+    assert_close("dK", to_np(tk.grad), wdk, FP32_TOL)
+    assert_close("dV", to_np(tv.grad), wdv, FP32_TOL)
