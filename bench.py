@@ -1,0 +1,241 @@
+"""FlexAttention benchmark on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--config c2|c3|c4|c5|ns] [--no-cpu]
+
+A step is one forward + backward pass (fa_fwd, fa_bwd_preprocess,
+fa_bwd_dkdv, fa_bwd_dq through the C ABI, outputs preallocated, inputs
+resident in HBM) over one batch of synthetic inputs.  Throughput counts only
+unmasked (query, key) pairs P per (batch, head): fwd 4*D*P, bwd 10*D*P,
+fwd+bwd 14*D*P FLOPs (recomputation is not credited).
+
+Prints ONE JSON line.  ``value`` is the fwd+bwd effective TFLOP/s; the line
+also carries the forward figure, per-kernel times, the roofline of the
+dominant kernel (HIP events on the launch stream) and the CPU baseline: the
+oracle's C restatement of the reference's tiled algorithm, timed on a bounded
+sample of heads of the same workload on this host.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "pallas-flexattn_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+
+METRIC = "effective TFLOP/s fwd and fwd+bwd (unmasked FLOPs), % of bf16 MFMA peak"
+PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA: 256 CU x 4 SIMD x 1024 FLOP/clk x 2.4 GHz ("2.5 PFLOP/s")
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def doc_lengths(rng, S):
+    out, tot = [], 0
+    while tot < S:
+        n = int(rng.integers(256, 4097))
+        n = min(n, S - tot)
+        out.append(n)
+        tot += n
+    return out
+
+
+def make_config(name):
+    """Workload definitions (shapes, masks, score mods, seeds)."""
+    import pallas_flexattn as pf
+    if name == "c2":
+        return dict(workload="causal fwd+bwd B8 H16 S2048 D128 bf16 (q,k,v ~ 0.5*N(0,1))", B=8, Hq=16, Hkv=16,
+                    S=2048, D=128, seed=1, scale_in=0.5, mask=pf.causal_mask, window=(-1, 0), docs=None,
+                    score=None)
+    if name == "c3":
+        return dict(workload="sliding-window-1024 causal fwd+bwd B4 H32 S8192 D128 bf16", B=4, Hq=32, Hkv=32,
+                    S=8192, D=128, seed=2, scale_in=1.0, mask=pf.sliding_window_mask(1023, 0),
+                    window=(1023, 0), docs=None, score=None)
+    if name == "c4":
+        return dict(workload="GQA causal + ALiBi + softcap50 fwd+bwd B4 Hq32 Hkv8 S4096 D128 bf16", B=4, Hq=32,
+                    Hkv=8, S=4096, D=128, seed=3, scale_in=1.0, mask=pf.causal_mask, window=(-1, 0), docs=None,
+                    score=pf.compose_score_mods(pf.alibi_score_mod(32), pf.softcap_score_mod(50.0)))
+    if name == "c5":
+        rng = np.random.default_rng(4)
+        lens = [doc_lengths(rng, 16384) for _ in range(2)]
+        dm = pf.document_mask(lens)
+        return dict(workload="packed-document causal fwd+bwd B2 H16 S16384 D128 bf16", B=2, Hq=16, Hkv=16,
+                    S=16384, D=128, seed=4, scale_in=1.0, mask=pf.and_masks(dm, pf.causal_mask), window=(-1, 0),
+                    docs=dm.doc_ids, score=None)
+    if name == "ns":
+        return dict(workload="causal fwd+bwd B4 H32 S8192 D128 bf16", B=4, Hq=32, Hkv=32, S=8192, D=128, seed=5,
+                    scale_in=1.0, mask=pf.causal_mask, window=(-1, 0), docs=None, score=None)
+    raise SystemExit(f"unknown config {name}")
+
+
+def count_pairs(cfg):
+    """Unmasked (q, k) pairs summed over batch rows, per head (exact)."""
+    S = cfg["S"]
+    left, right = cfg["window"]
+    q = np.arange(S, dtype=np.int64)
+    lo = np.zeros(S, np.int64) if left < 0 else np.maximum(q - left, 0)
+    hi = np.full(S, S - 1, np.int64) if right < 0 else np.minimum(q + right, S - 1)
+    if cfg["docs"] is None:
+        return int(np.sum(hi - lo + 1)) * cfg["B"]
+    total = 0
+    for b in range(cfg["B"]):
+        d = cfg["docs"][min(b, cfg["docs"].shape[0] - 1)]
+        starts = np.searchsorted(d, d, side="left")
+        ends = np.searchsorted(d, d, side="right") - 1
+        a, z = np.maximum(lo, starts), np.minimum(hi, ends)
+        total += int(np.sum(np.maximum(z - a + 1, 0)))
+    return total
+
+
+def gen_inputs(cfg):
+    rng = np.random.default_rng(cfg["seed"])
+    B, Hq, Hkv, S, D = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["S"], cfg["D"]
+    q = rng.standard_normal((B, Hq, S, D), dtype=np.float32) * cfg["scale_in"]
+    k = rng.standard_normal((B, Hkv, S, D), dtype=np.float32) * cfg["scale_in"]
+    v = rng.standard_normal((B, Hkv, S, D), dtype=np.float32) * cfg["scale_in"]
+    do = rng.standard_normal((B, Hq, S, D), dtype=np.float32)
+    return q, k, v, do
+
+
+def time_region(fn, iters, stream):
+    import torch
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(iters):
+        fn()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+def cpu_baseline(cfg, arrays, pairs_per_head, target_s):
+    """The oracle's C restatement of the reference's tiled fwd + 3-kernel bwd
+    (every tile computed, as the reference does), on a bounded sample of
+    (batch, head) programs."""
+    from oracle import tiled
+    from oracle.bf16 import round_bf16
+    B, Hq, S, D = cfg["B"], cfg["Hq"], cfg["S"], cfg["D"]
+    if cfg["Hq"] != cfg["Hkv"] or cfg["score"] is not None or cfg["docs"] is not None:
+        return None  # the reference algorithm has no GQA / score mods / document masks
+    q, k, v, do = (round_bf16(a) for a in arrays)
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count() or 1
+    threads = min(threads, os.cpu_count() or threads)
+
+    def run(nh):
+        t0 = time.perf_counter()
+        o, lse = tiled.fwd(q, k, v, 128, 64, window=cfg["window"], bf16=True, nthreads=threads, bh_range=(0, nh))
+        tiled.bwd(q, k, v, o, lse, do, 128, 64, window=cfg["window"], bf16=True, nthreads=threads,
+                  bh_range=(0, nh))
+        return time.perf_counter() - t0
+
+    t1 = run(min(threads, B * Hq))
+    per_head = t1 / min(threads, B * Hq)
+    nh = int(max(1, min(B * Hq, target_s / max(per_head, 1e-6))))
+    nh = max(min(threads, B * Hq), (nh // threads) * threads) if nh >= threads else nh
+    t = run(nh)
+    flops = 14.0 * D * pairs_per_head * nh / B  # pairs_per_head sums over batch rows
+    return {"value": flops / t / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{nh} of {B * Hq} (batch, head) programs, fwd + 3-kernel bwd over all tiles, "
+                      f"{t:.1f} s; same unmasked-FLOP count as the GPU value"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c2")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported (run with --gpus 1)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import pallas_flexattn as pf
+    from pallas_flexattn.flash_attn import Runner
+
+    cfg = make_config(args.config)
+    B, Hq, Hkv, S, D = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["S"], cfg["D"]
+    log(f"config {args.config}: {cfg['workload']}")
+    arrays = gen_inputs(cfg)
+    dev = torch.device("cuda:0")
+    tq, tk, tv, tdo = (torch.from_numpy(a).to(dev, torch.bfloat16) for a in arrays)
+    t0 = time.perf_counter()
+    bmask = pf.create_block_mask(cfg["mask"], B, Hq, S, S, 128)
+    mask_ms = (time.perf_counter() - t0) * 1e3
+    runner = Runner(tq, tk, tv, tdo, score_mod=cfg["score"], block_mask=bmask)
+    pairs = count_pairs(cfg)  # per head, summed over batch rows
+    flop_fwd = 4.0 * D * pairs * Hq
+    flop_bwd = 10.0 * D * pairs * Hq
+    stream = torch.cuda.current_stream()
+
+    for _ in range(args.warmup):
+        runner.step()
+    torch.cuda.synchronize()
+    log(f"warmup done ({args.warmup} steps)")
+    torch.cuda.synchronize()
+    ms_step = time_region(runner.step, args.steps, stream)
+    torch.cuda.synchronize()
+    log(f"timed {args.steps} steps: {ms_step:.3f} ms/step")
+
+    kernels = {}
+    for name, fn in (("fwd", runner.fwd), ("bwd_preprocess", runner.preprocess), ("bwd_dkdv", runner.dkdv),
+                     ("bwd_dq", runner.dq_)):
+        fn()
+        kernels[name] = time_region(fn, args.steps, stream)
+    ms_fwd = kernels["fwd"]
+    algo = {"fwd": flop_fwd, "bwd_dkdv": 8.0 * D * pairs * Hq, "bwd_dq": 6.0 * D * pairs * Hq}
+    dom = max(("fwd", "bwd_dkdv", "bwd_dq"), key=lambda n: kernels[n])
+    achieved = algo[dom] / (kernels[dom] * 1e-3) / 1e12
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get(f"{args.config}/{dom}")
+    fwdbwd_tflops = (flop_fwd + flop_bwd) / (ms_step * 1e-3) / 1e12
+    fwd_tflops = flop_fwd / (ms_fwd * 1e-3) / 1e12
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        cpu = cpu_baseline(cfg, arrays, pairs, args.cpu_seconds)
+        log("cpu baseline done")
+
+    out = {
+        "metric": METRIC,
+        "value": round(fwdbwd_tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded numpy normals rounded to bf16)",
+        "config": {"workload": cfg["workload"], "B": B, "Hq": Hq, "Hkv": Hkv, "S": S, "D": D,
+                   "mask_block": 128, "live_tiles": bmask.live_tiles(),
+                   "unmasked_pairs_per_head": pairs / B},
+        "fwdbwd_pct_peak": round(100 * fwdbwd_tflops / PEAK_BF16_TFLOPS, 2),
+        "fwd_tflops": round(fwd_tflops, 2),
+        "fwd_pct_peak": round(100 * fwd_tflops / PEAK_BF16_TFLOPS, 2),
+        "kernel_ms": {k: round(v, 4) for k, v in kernels.items()},
+        "block_mask_build_ms": round(mask_ms, 2),
+        "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

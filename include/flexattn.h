@@ -102,6 +102,17 @@ int fa_bwd(const fa_params *p, const void *q, const void *k, const void *v, cons
            const float *lse, const void *dout, void *dq, void *dk, void *dv, void *workspace,
            size_t workspace_bytes, void *stream);
 
+/* The three stages fa_bwd runs, callable one at a time (the reference exposes
+ * the same split as flash_attention_bwd_preprocess / _dkv / _dq).
+ *   fa_bwd_preprocess — flash_attn.py:168-203: delta[b][h][q] = sum_d o * dout (fp32, (B, Hq, Sq))
+ *   fa_bwd_dkdv       — flash_attn.py:206-310: dK, dV (walks the q-side tables)
+ *   fa_bwd_dq         — flash_attn.py:313-407: dQ (walks the kv-side tables)  */
+int fa_bwd_preprocess(const fa_params *p, const void *o, const void *dout, float *delta, void *stream);
+int fa_bwd_dkdv(const fa_params *p, const void *q, const void *k, const void *v, const void *dout,
+                const float *lse, const float *delta, void *dk, void *dv, void *stream);
+int fa_bwd_dq(const fa_params *p, const void *q, const void *k, const void *v, const void *dout,
+              const float *lse, const float *delta, void *dq, void *stream);
+
 const char *fa_strerror(int status);
 int fa_abi_version(void);
 

@@ -142,22 +142,47 @@ int run_delta(const BwdArgs& a, hipStream_t s) {
   return launch_status();
 }
 
+enum { kStageDelta = 1, kStageDkdv = 2, kStageDq = 4 };
+
 template <typename T, int D, int BN, int BQ, bool M>
-int bwd_all(const BwdArgs& a, int bm, hipStream_t s) {
-  int rc = run_delta<T, D>(a, s);
-  if (rc) return rc;
-  rc = run_dkdv<T, D, BQ, 4, M>(a, s);
-  if (rc) return rc;
-  return bm == 64 ? run_dq<T, D, BN, 2, M>(a, s) : run_dq<T, D, BN, 4, M>(a, s);
+int bwd_all(const BwdArgs& a, int bm, int stages, hipStream_t s) {
+  int rc = FA_OK;
+  if (stages & kStageDelta) rc = run_delta<T, D>(a, s);
+  if (!rc && (stages & kStageDkdv)) rc = run_dkdv<T, D, BQ, 4, M>(a, s);
+  if (!rc && (stages & kStageDq))
+    rc = bm == 64 ? run_dq<T, D, BN, 2, M>(a, s) : run_dq<T, D, BN, 4, M>(a, s);
+  return rc;
 }
 
 template <typename T, int BN, int BQ, bool M>
-int bwd_d(const BwdArgs& a, int D, int bm, hipStream_t s) {
+int bwd_d(const BwdArgs& a, int D, int bm, int stages, hipStream_t s) {
   switch (D) {
-    case 32: return bwd_all<T, 32, BN, BQ, M>(a, bm, s);
-    case 64: return bwd_all<T, 64, BN, BQ, M>(a, bm, s);
-    default: return bwd_all<T, 128, BN, BQ, M>(a, bm, s);
+    case 32: return bwd_all<T, 32, BN, BQ, M>(a, bm, stages, s);
+    case 64: return bwd_all<T, 64, BN, BQ, M>(a, bm, stages, s);
+    default: return bwd_all<T, 128, BN, BQ, M>(a, bm, stages, s);
   }
+}
+
+// Validates the params for the requested backward stages and launches them.
+int bwd_stages(const fa_params* p, BwdArgs& a, int stages, hipStream_t s) {
+  if (!p) return FA_ERR_NULL;
+  Tiles t;
+  int rc = default_tiles(p, &t);
+  if (rc) return rc;
+  rc = build_problem(p, t, &a.p);
+  if (rc) return rc;
+  if (a.p.has_tables && (stages & (kStageDkdv | kStageDq))) {
+    if (a.p.mblk_q % t.bm || a.p.mblk_kv % t.bn || a.p.mblk_kv % t.bkv || a.p.mblk_q % t.bq)
+      return FA_ERR_TABLES;
+    if ((stages & kStageDq) && !a.p.kv_num && !a.p.full_kv_num) return FA_ERR_TABLES;
+    if ((stages & kStageDkdv) && !a.p.q_num && !a.p.full_q_num) return FA_ERR_TABLES;
+  }
+  const bool m = has_mods(a.p);
+  if (p->dtype == FA_DTYPE_BF16)
+    return m ? bwd_d<uint16_t, 64, 64, true>(a, p->D, t.bm, stages, s)
+             : bwd_d<uint16_t, 64, 64, false>(a, p->D, t.bm, stages, s);
+  return m ? bwd_d<float, 32, 32, true>(a, p->D, t.bm, stages, s)
+           : bwd_d<float, 32, 32, false>(a, p->D, t.bm, stages, s);
 }
 
 size_t delta_bytes(const fa_params* p) {
@@ -218,20 +243,9 @@ int fa_bwd(const fa_params* p, const void* q, const void* k, const void* v, cons
            const float* lse, const void* dout, void* dq, void* dk, void* dv, void* workspace,
            size_t workspace_bytes, void* stream) {
   if (!p) return FA_ERR_NULL;
-  Tiles t;
-  int rc = default_tiles(p, &t);
-  if (rc) return rc;
-  BwdArgs a;
-  rc = build_problem(p, t, &a.p);
-  if (rc) return rc;
   if (!q || !k || !v || !o || !lse || !dout || !dq || !dk || !dv) return FA_ERR_NULL;
   if (!workspace || workspace_bytes < delta_bytes(p)) return FA_ERR_WORKSPACE;
-  if (a.p.has_tables) {
-    if (a.p.mblk_q % t.bm || a.p.mblk_kv % t.bn || a.p.mblk_kv % t.bkv || a.p.mblk_q % t.bq)
-      return FA_ERR_TABLES;
-    if (!a.p.kv_num && !a.p.full_kv_num) return FA_ERR_TABLES;
-    if (!a.p.q_num && !a.p.full_q_num) return FA_ERR_TABLES;
-  }
+  BwdArgs a{};
   a.q = q;
   a.k = k;
   a.v = v;
@@ -242,11 +256,48 @@ int fa_bwd(const fa_params* p, const void* q, const void* k, const void* v, cons
   a.dk = dk;
   a.dv = dv;
   a.delta = static_cast<float*>(workspace);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool m = has_mods(a.p);
-  if (p->dtype == FA_DTYPE_BF16)
-    return m ? bwd_d<uint16_t, 64, 64, true>(a, p->D, t.bm, s) : bwd_d<uint16_t, 64, 64, false>(a, p->D, t.bm, s);
-  return m ? bwd_d<float, 32, 32, true>(a, p->D, t.bm, s) : bwd_d<float, 32, 32, false>(a, p->D, t.bm, s);
+  return bwd_stages(p, a, kStageDelta | kStageDkdv | kStageDq, static_cast<hipStream_t>(stream));
+}
+
+int fa_bwd_preprocess(const fa_params* p, const void* o, const void* dout, float* delta, void* stream) {
+  if (!p) return FA_ERR_NULL;
+  if (!o || !dout || !delta) return FA_ERR_NULL;
+  BwdArgs a{};
+  a.o = o;
+  a.dout = dout;
+  a.delta = delta;
+  return bwd_stages(p, a, kStageDelta, static_cast<hipStream_t>(stream));
+}
+
+int fa_bwd_dkdv(const fa_params* p, const void* q, const void* k, const void* v, const void* dout,
+                const float* lse, const float* delta, void* dk, void* dv, void* stream) {
+  if (!p) return FA_ERR_NULL;
+  if (!q || !k || !v || !dout || !lse || !delta || !dk || !dv) return FA_ERR_NULL;
+  BwdArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.dout = dout;
+  a.lse = lse;
+  a.delta = const_cast<float*>(delta);
+  a.dk = dk;
+  a.dv = dv;
+  return bwd_stages(p, a, kStageDkdv, static_cast<hipStream_t>(stream));
+}
+
+int fa_bwd_dq(const fa_params* p, const void* q, const void* k, const void* v, const void* dout,
+              const float* lse, const float* delta, void* dq, void* stream) {
+  if (!p) return FA_ERR_NULL;
+  if (!q || !k || !v || !dout || !lse || !delta || !dq) return FA_ERR_NULL;
+  BwdArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.dout = dout;
+  a.lse = lse;
+  a.delta = const_cast<float*>(delta);
+  a.dq = dq;
+  return bwd_stages(p, a, kStageDq, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -8,6 +8,9 @@ from pallas_flexattn.flash_attn import (
     flash_attention_bwd,
     mha_reference,
     flex_attention,
+    flash_attention_bwd_preprocess,
+    flash_attention_bwd_dkv,
+    flash_attention_bwd_dq,
 )
 from pallas_flexattn.mask_mod import (
     MaskMod,
@@ -57,6 +60,9 @@ __all__ = [
     "print_kernel_config",
     # MI355X FlexAttention surface
     "flex_attention",
+    "flash_attention_bwd_preprocess",
+    "flash_attention_bwd_dkv",
+    "flash_attention_bwd_dq",
     "MaskSpec",
     "document_mask",
     "document_ids_mask",

@@ -39,7 +39,8 @@ class FaParams(ctypes.Structure):
     ]
 
 
-EXPORTED = ("fa_fwd", "fa_bwd", "fa_bwd_workspace_bytes", "fa_strerror", "fa_abi_version")
+EXPORTED = ("fa_fwd", "fa_bwd", "fa_bwd_workspace_bytes", "fa_bwd_preprocess", "fa_bwd_dkdv", "fa_bwd_dq",
+            "fa_strerror", "fa_abi_version")
 
 _lib = None
 
@@ -64,6 +65,12 @@ def load():
     lib.fa_fwd.restype = ctypes.c_int
     lib.fa_bwd.argtypes = [P, v, v, v, v, v, v, v, v, v, v, ctypes.c_size_t, v]
     lib.fa_bwd.restype = ctypes.c_int
+    lib.fa_bwd_preprocess.argtypes = [P, v, v, v, v]
+    lib.fa_bwd_preprocess.restype = ctypes.c_int
+    lib.fa_bwd_dkdv.argtypes = [P, v, v, v, v, v, v, v, v, v]
+    lib.fa_bwd_dkdv.restype = ctypes.c_int
+    lib.fa_bwd_dq.argtypes = [P, v, v, v, v, v, v, v, v]
+    lib.fa_bwd_dq.restype = ctypes.c_int
     lib.fa_bwd_workspace_bytes.argtypes = [P]
     lib.fa_bwd_workspace_bytes.restype = ctypes.c_size_t
     lib.fa_strerror.argtypes = [ctypes.c_int]

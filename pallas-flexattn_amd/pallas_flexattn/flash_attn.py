@@ -231,6 +231,127 @@ def _ref_tiles(q, block_r, block_c):
     return kernel_tiles(block_r, block_c, dname)
 
 
+def _as4d(t):
+    """(B*H, T, C) flattened arrays of the reference's stage functions -> (B*H, 1, T, C)."""
+    return t.unsqueeze(1) if t.dim() == 3 else t
+
+
+def _stage_plan(q4, k4, mask_mod, block_r, block_c, scale=None):
+    mask = _as_mask_spec(mask_mod)
+    bm = None
+    if mask is not None and not mask.is_trivial:
+        bm = _internal_block_mask(mask, q4.shape[0], q4.shape[2], k4.shape[2])
+    return _Plan(q4, k4, mask, None, scale, bm, _ref_tiles(q4, block_r, block_c))
+
+
+def flash_attention_bwd_preprocess(o_flat, do_flat, block_r: int = DEFAULT_BLOCK_R,
+                                   num_warps: int = DEFAULT_NUM_WARPS, num_stages: int = DEFAULT_NUM_STAGES,
+                                   interpret: bool = False):
+    """Delta = rowsum(O * dO) (``flash_attn.py:168-203``), shape o.shape[:-1].
+    Returned in fp32 (the reference stores it in O's dtype)."""
+    _check_interpret(interpret)
+    torch = _torch()
+    o4, do4 = _dense16(_as4d(o_flat)), _dense16(_as4d(do_flat).to(o_flat.dtype))
+    plan = _stage_plan(o4, o4, None, block_r, DEFAULT_BLOCK_C)
+    delta = torch.empty(o4.shape[:3], device=o4.device, dtype=torch.float32)
+    _lib.check(_lib.load().fa_bwd_preprocess(plan.ptr(), o4.data_ptr(), do4.data_ptr(), delta.data_ptr(),
+                                             _stream()))
+    return delta.reshape(o_flat.shape[:-1])
+
+
+def _stage_inputs(q_flat, k_flat, v_flat, do_flat, logsumexp_flat, d_flat, qk_scale, softmax_scale):
+    torch = _torch()
+    if abs(qk_scale - softmax_scale) > 1e-12 * max(abs(qk_scale), 1.0):
+        raise NotImplementedError("the kernels apply one softmax scale to both S and dS")
+    q4, k4, v4 = (_dense16(_as4d(t)) for t in (q_flat, k_flat, v_flat))
+    _check_inputs(q4, k4, v4)
+    do4 = _dense16(_as4d(do_flat).to(q4.dtype))
+    lse = logsumexp_flat.to(torch.float32).reshape(q4.shape[:3]).contiguous()
+    delta = d_flat.to(torch.float32).reshape(q4.shape[:3]).contiguous()
+    return q4, k4, v4, do4, lse, delta
+
+
+def flash_attention_bwd_dkv(q_flat, k_flat, v_flat, do_flat, logsumexp_flat, d_flat, qk_scale: float,
+                            softmax_scale: float, block_r: int = DEFAULT_BLOCK_R, block_c: int = DEFAULT_BLOCK_C,
+                            num_warps: int = DEFAULT_NUM_WARPS, num_stages: int = DEFAULT_NUM_STAGES,
+                            mask_mod: Optional[MaskMod] = None, interpret: bool = False):
+    """dK, dV (``flash_attn.py:206-310``) from q, k, v, dO, LSE and Delta."""
+    _check_interpret(interpret)
+    torch = _torch()
+    q4, k4, v4, do4, lse, delta = _stage_inputs(q_flat, k_flat, v_flat, do_flat, logsumexp_flat, d_flat,
+                                                qk_scale, softmax_scale)
+    plan = _stage_plan(q4, k4, mask_mod, block_r, block_c, qk_scale)
+    dk, dv = torch.empty_like(k4), torch.empty_like(v4)
+    _lib.check(_lib.load().fa_bwd_dkdv(plan.ptr(), q4.data_ptr(), k4.data_ptr(), v4.data_ptr(), do4.data_ptr(),
+                                       lse.data_ptr(), delta.data_ptr(), dk.data_ptr(), dv.data_ptr(), _stream()))
+    return dk.reshape(k_flat.shape), dv.reshape(v_flat.shape)
+
+
+def flash_attention_bwd_dq(q_flat, k_flat, v_flat, do_flat, logsumexp_flat, d_flat, qk_scale: float,
+                           softmax_scale: float, block_r: int = DEFAULT_BLOCK_R, block_c: int = DEFAULT_BLOCK_C,
+                           num_warps: int = DEFAULT_NUM_WARPS, num_stages: int = DEFAULT_NUM_STAGES,
+                           mask_mod: Optional[MaskMod] = None, interpret: bool = False):
+    """dQ (``flash_attn.py:313-407``) from q, k, v, dO, LSE and Delta."""
+    _check_interpret(interpret)
+    torch = _torch()
+    q4, k4, v4, do4, lse, delta = _stage_inputs(q_flat, k_flat, v_flat, do_flat, logsumexp_flat, d_flat,
+                                                qk_scale, softmax_scale)
+    plan = _stage_plan(q4, k4, mask_mod, block_r, block_c, qk_scale)
+    dq = torch.empty_like(q4)
+    _lib.check(_lib.load().fa_bwd_dq(plan.ptr(), q4.data_ptr(), k4.data_ptr(), v4.data_ptr(), do4.data_ptr(),
+                                     lse.data_ptr(), delta.data_ptr(), dq.data_ptr(), _stream()))
+    return dq.reshape(q_flat.shape)
+
+
+class Runner:
+    """Pre-planned kernel launches for repeated calls on fixed shapes (used by
+    the benchmark): the fa_params struct, block tables and outputs are built
+    once; each call only enqueues kernels on the current stream."""
+
+    def __init__(self, q, k, v, do, mask_mod=None, score_mod=None, block_mask=None, scale=None, tiles=None):
+        torch = _torch()
+        _check_inputs(q, k, v)
+        self.q, self.k, self.v = _dense16(q), _dense16(k), _dense16(v)
+        self.do = _dense16(do)
+        mask = _as_mask_spec(mask_mod if block_mask is None else block_mask.mask_mod)
+        if block_mask is None and mask is not None and not mask.is_trivial:
+            block_mask = _internal_block_mask(mask, q.shape[0], q.shape[2], k.shape[2])
+        _, dname = _dtype_code(q)
+        tiles = tiles or (128, 64 if dname == "bf16" else 32)
+        self.plan = _Plan(self.q, self.k, mask, _as_score_spec(score_mod), scale, block_mask, tiles)
+        self.block_mask = block_mask
+        self.o = torch.empty_like(self.q)
+        self.lse = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
+        self.delta = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
+        self.dq, self.dk, self.dv = torch.empty_like(self.q), torch.empty_like(self.k), torch.empty_like(self.v)
+        self.lib = _lib.load()
+
+    def fwd(self):
+        _lib.check(self.lib.fa_fwd(self.plan.ptr(), self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
+                                   self.o.data_ptr(), self.lse.data_ptr(), _stream()))
+
+    def preprocess(self):
+        _lib.check(self.lib.fa_bwd_preprocess(self.plan.ptr(), self.o.data_ptr(), self.do.data_ptr(),
+                                              self.delta.data_ptr(), _stream()))
+
+    def dkdv(self):
+        _lib.check(self.lib.fa_bwd_dkdv(self.plan.ptr(), self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
+                                        self.do.data_ptr(), self.lse.data_ptr(), self.delta.data_ptr(),
+                                        self.dk.data_ptr(), self.dv.data_ptr(), _stream()))
+
+    def dq_(self):
+        _lib.check(self.lib.fa_bwd_dq(self.plan.ptr(), self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
+                                      self.do.data_ptr(), self.lse.data_ptr(), self.delta.data_ptr(),
+                                      self.dq.data_ptr(), _stream()))
+
+    def step(self):
+        """One forward + backward pass."""
+        self.fwd()
+        self.preprocess()
+        self.dkdv()
+        self.dq_()
+
+
 # ------------------------------------------------------------ public API ----
 def mha_reference(q, k, v, mask_mod: Optional[MaskMod] = None):
     """Materialised attention (``flash_attn.py:33-56``): ``softmax(where(mask,
