@@ -1,0 +1,76 @@
+"""The C ABI library (CPU): it loads, exports every function include/flexattn.h
+declares, and rejects bad arguments before touching the GPU."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from pallas_flexattn import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "flexattn.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char \*)\s*(fa_\w+)\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_functions()
+    assert set(names) == set(_lib.EXPORTED)
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_abi_version_and_strerror():
+    lib = _lib.load()
+    assert lib.fa_abi_version() == _lib.ABI_VERSION
+    assert lib.fa_strerror(0) == b"success"
+    for code in range(-8, 0):
+        assert lib.fa_strerror(code) != b"unknown status"
+
+
+def test_params_struct_layout_matches_header():
+    # 12 int32 + float + 2 int32, then pointers (8-byte aligned) ... computed from the header order
+    p = _lib.FaParams
+    assert p.scale.offset == 40 and p.q_doc_ids.offset == 56
+    assert ctypes.sizeof(p) == p.full_q_indices.offset + 8
+
+
+def _params(**kw):
+    p = _lib.FaParams()
+    p.abi_version = _lib.ABI_VERSION
+    p.dtype = _lib.DTYPE_BF16
+    p.B, p.Hq, p.Hkv, p.Sq, p.Skv, p.D = 1, 2, 2, 128, 128, 128
+    p.window_left = p.window_right = -1
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(abi_version=99), -8), (dict(dtype=7), -3), (dict(D=48), -4), (dict(Hq=3, Hkv=2), -2),
+    (dict(Sq=0), -2), (dict(block_m=96), -4), (dict(softcap=-1.0), -2),
+    (dict(q_doc_ids=1234), -1),
+    (dict(kv_num_blocks=8, kv_indices=8, mask_block_q=0, mask_block_kv=128), -5),
+    (dict(kv_num_blocks=8, kv_indices=8, mask_block_q=128, mask_block_kv=128, table_b=3, table_h=1), -5),
+])
+def test_fwd_rejects_bad_params_before_any_launch(kw, code):
+    lib = _lib.load()
+    dummy = ctypes.c_void_p(16)
+    p = _params(**kw)
+    assert lib.fa_fwd(ctypes.byref(p), dummy, dummy, dummy, dummy, dummy, None) == code
+
+
+def test_null_pointers_and_small_workspace_rejected():
+    lib = _lib.load()
+    p = _params()
+    d = ctypes.c_void_p(16)
+    assert lib.fa_fwd(ctypes.byref(p), None, d, d, d, d, None) == -1
+    assert lib.fa_fwd(None, d, d, d, d, d, None) == -1
+    need = lib.fa_bwd_workspace_bytes(ctypes.byref(p))
+    assert need >= 2 * 128 * 4
+    assert lib.fa_bwd(ctypes.byref(p), d, d, d, d, d, d, d, d, d, d, need - 1, None) == -6
+    assert lib.fa_bwd_dq(ctypes.byref(p), d, d, d, d, d, None, d, None) == -1

@@ -1,0 +1,56 @@
+"""Kernel tuner (CPU): the reference's invariants (``tests/test_kernel_tuner.py``)
+plus the exact threshold table of ``kernel_tuner.py:28-63`` and the mapping
+onto the MI355X tiles."""
+import pytest
+
+from pallas_flexattn import get_kernel_config, get_optimal_params
+from pallas_flexattn.kernel_tuner import SUPPORTED_BLOCK_M, kernel_tiles
+
+
+class TestKernelTuner:
+    def test_get_optimal_params_short_sequence(self):
+        block_r, block_c, num_warps, num_stages = get_optimal_params(256, 64)
+        assert block_r <= 64 and block_c <= 64 and num_warps >= 4
+
+    def test_get_optimal_params_long_sequence(self):
+        block_r, block_c, num_warps, num_stages = get_optimal_params(4096, 64)
+        assert block_r >= 128 and block_c >= 64 and num_warps >= 8
+
+    def test_get_optimal_params_large_head_dim(self):
+        block_r, block_c, _, _ = get_optimal_params(2048, 256)
+        assert block_r <= 64 and block_c <= 64
+
+    def test_get_optimal_params_cached(self):
+        assert get_optimal_params(1024, 64) == get_optimal_params(1024, 64)
+        assert get_optimal_params.cache_info().hits >= 1
+
+    def test_get_kernel_config(self):
+        config = get_kernel_config(2, 8, 2048, 64, 'causal')
+        assert config['batch_size'] == 2 and config['num_heads'] == 8
+        assert config['seq_len'] == 2048 and config['head_dim'] == 64
+        for key in ('block_r', 'block_c', 'num_warps', 'num_stages'):
+            assert key in config
+
+    def test_sparsity_optimization(self):
+        assert get_kernel_config(2, 8, 1024, 64, 'causal')['block_r'] <= get_kernel_config(2, 8, 1024, 64, None)['block_r']
+
+
+# the reference's table, restated as literal rows (kernel_tuner.py:28-63)
+@pytest.mark.parametrize("seq,d,sparse,want", [
+    (256, 64, False, (32, 32, 4, 2)), (512, 64, False, (64, 64, 4, 3)), (2048, 64, False, (128, 64, 4, 3)),
+    (4096, 64, False, (128, 128, 8, 4)), (8192, 64, False, (128, 128, 8, 5)),
+    (2048, 256, False, (64, 64, 4, 3)), (8192, 256, False, (64, 64, 8, 3)),
+    (256, 32, False, (32, 32, 4, 4)), (8192, 32, False, (128, 128, 8, 5)),
+    (2048, 128, True, (64, 64, 4, 3)), (8192, 128, True, (64, 64, 8, 5)), (4096, 128, True, (64, 64, 8, 4)),
+])
+def test_threshold_table(seq, d, sparse, want):
+    assert get_optimal_params(seq, d, sparse) == want
+
+
+def test_kernel_tile_mapping():
+    assert kernel_tiles(128, 64, "bf16") == (128, 64)
+    assert kernel_tiles(64, 64, "bf16") == (64, 64)
+    assert kernel_tiles(32, 32, "bf16") == (64, 64)
+    assert kernel_tiles(128, 128, "fp32") == (128, 32)
+    for br in (32, 64, 128, 256):
+        assert kernel_tiles(br, 64, "bf16")[0] in SUPPORTED_BLOCK_M
