@@ -4,6 +4,7 @@
 
 #include "../../include/flexattn.h"
 #include "bwd.h"
+#include "fwd_bf16.h"
 
 namespace {
 
@@ -99,7 +100,12 @@ int launch_status() { return hipGetLastError() == hipSuccess ? FA_OK : FA_ERR_LA
 template <typename T, int D, int BN, int NW, bool M>
 int run_fwd(const FwdArgs& a, hipStream_t s) {
   const int grid = a.p.B * a.p.Hq * cdiv(a.p.Sq, 32 * NW);
-  hipLaunchKernelGGL((fa::fwd_kernel<T, D, BN, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
+  if constexpr (sizeof(T) == 2) {
+    // bf16: LDS-DMA + transposing-read kernel
+    hipLaunchKernelGGL((fa::fwd_bf16_kernel<D, BN, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((fa::fwd_kernel<T, D, BN, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
+  }
   return launch_status();
 }
 

@@ -1,0 +1,49 @@
+// Buffer-resource loads for gfx950: branch-free bounds handling (reads past
+// the resource's byte range return zero) and direct HBM -> LDS copies.
+#pragma once
+#include "common.h"
+
+namespace fa {
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+#define FA_LDS __attribute__((address_space(3)))
+
+__device__ i32x4 raw_buffer_load_b128(i32x4 rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.v4i32");
+__device__ void raw_buffer_load_lds(i32x4 rsrc, FA_LDS uint32_t* lds, int size, int voffset, int soffset,
+                                    int offset, int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
+
+// 128-bit buffer descriptor: base address, byte range, gfx9 data-format word.
+__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  r[1] = __builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
+  r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+  r[3] = 0x00020000;
+  return r;
+}
+
+__device__ __forceinline__ u32x4 buf_load16(i32x4 rsrc, int byte_off) {
+  return __builtin_bit_cast(u32x4, raw_buffer_load_b128(rsrc, byte_off, 0, 0));
+}
+
+// Copy 16 bytes per lane from the buffer at byte_off into LDS at
+// lds_wave_base + 16 * lane (lds_wave_base must be wave-uniform).
+__device__ __forceinline__ void dma16(i32x4 rsrc, int byte_off, char* lds_wave_base) {
+  raw_buffer_load_lds(rsrc, (FA_LDS uint32_t*)(lds_wave_base), 16, byte_off, 0, 0, 0);
+}
+
+__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// ds_read_b64_tr_b16: within each group of 16 lanes, source lane s supplies the
+// address of 4 consecutive 16-bit elements (row s/4 of a 4x16 block at column
+// 4*(s%4)); lane j receives column j of that block, i.e. the 4 elements
+// (row t, column j) for t = 0..3.
+__device__ __forceinline__ uint2 lds_read_tr16(const char* p) {
+  s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FA_LDS s16x4*)(p));
+  return __builtin_bit_cast(uint2, v);
+}
+
+}  // namespace fa

@@ -1,0 +1,251 @@
+// bf16 forward FlexAttention kernel for gfx950 (the main forward path).
+//
+// Work item: (batch, q head, BM = 32*NW query rows); wave w owns rows
+// q0 + 32w .. +31 for the whole kv walk.
+//
+// Per kv tile of BN keys (double-buffered in LDS, one barrier per tile):
+//   * K and V tiles are copied HBM -> LDS with buffer_load ... lds (no
+//     registers, no bounds branches: rows past the sequence read as zero),
+//     issued one tile ahead;
+//   * S^T = K Q^T   (A = K rows from LDS in perm23 order, B = Q from VGPRs);
+//   * online softmax with one query per lane: row max / sum are per-lane
+//     scalars plus one exchange between lane halves; O is rescaled only when
+//     some row maximum grew (multiplying by exp2(0) = 1 is skipped, so results
+//     are unchanged);
+//   * O^T += V^T P^T (A = V^T fetched from the row-major V tile with
+//     ds_read_b64_tr_b16, B = P^T straight from the S^T accumulators).
+// LDS layouts (row = key, 16-byte chunks): K chunk c of row r sits in slot
+// c ^ ((r + 4*(r>>3)) & 7) — the 32 rows read together by an A-operand load
+// land in distinct banks; V chunk c sits in slot c ^ (r & 3) — the 4
+// consecutive rows of one transposing read land in distinct banks.
+#pragma once
+#include "dma.h"
+#include "fwd.h"
+
+namespace fa {
+
+template <int D, int BN, int NW, bool kMods>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
+void fwd_bf16_kernel(FwdArgs a) {
+  using E = Elt<uint16_t>;
+  using frag = E::frag;
+  constexpr int BM = 32 * NW;
+  constexpr int RB = D * 2;             // bytes per row
+  constexpr int KCH = D / 8;            // 16-byte chunks per row
+  constexpr int KSTEPS = D / 16;
+  constexpr int NSUB = BN / 32;
+  constexpr int DT = D / 32;
+  constexpr int TILE = BN * RB;         // bytes per K (or V) tile
+  constexpr int IPW = TILE / 1024 / NW; // DMA instructions per wave per tile
+  constexpr int KMASK = (KCH >= 8 ? 8 : KCH) - 1;
+  static_assert(KCH >= 4 && D % 32 == 0 && BN % 32 == 0, "tile shape");
+  static_assert(TILE % (1024 * NW) == 0, "DMA split");
+
+  __shared__ __attribute__((aligned(1024))) char lds[4 * TILE];  // K0 K1 V0 V1
+
+  const Problem& P = a.p;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int lr = lane & 31, hh = lane >> 5;
+  const int nqt = (P.Sq + BM - 1) / BM;
+  int head, qt;
+  work_item(blockIdx.x, P.B * P.Hq, nqt, P.xcd_remap, &head, &qt);
+  const int b = head / P.Hq, h = head - b * P.Hq;
+  const int hk = h / (P.Hq / P.Hkv);
+  const int q0 = qt * BM;
+  const int qw = q0 + 32 * w + lr;
+  const bool qvalid = qw < P.Sq;
+
+  const char* kbase_ptr = static_cast<const char*>(a.k) + (size_t)(b * P.Hkv + hk) * P.Skv * RB;
+  const char* vbase_ptr = static_cast<const char*>(a.v) + (size_t)(b * P.Hkv + hk) * P.Skv * RB;
+
+  // Q rows as B operands (rows past the sequence read as zero)
+  frag qf[KSTEPS];
+  {
+    const i32x4 rq = make_rsrc(static_cast<const char*>(a.q) + (size_t)head * P.Sq * RB, (uint32_t)P.Sq * RB);
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) qf[s] = buf_load16(rq, qw * RB + (2 * s + hh) * 16);
+  }
+  const float slope = P.alibi ? P.alibi[h] : 0.f;
+  const int qdoc = (P.q_doc && qvalid) ? P.q_doc[(size_t)b * P.Sq + qw] : 0;
+
+  // loop-invariant LDS / global offsets
+  int dma_off_k[IPW], dma_off_v[IPW], dma_row[IPW];
+#pragma unroll
+  for (int u = 0; u < IPW; ++u) {
+    const int g = (w * IPW + u) * 64 + lane;
+    const int r = g / KCH, p = g % KCH;
+    dma_row[u] = r;
+    dma_off_k[u] = r * RB + ((p ^ ((r + 4 * (r >> 3)) & KMASK)) * 16);
+    dma_off_v[u] = r * RB + ((p ^ (r & 3)) * 16);
+  }
+  int koffA[KSTEPS];
+  {
+    const int r = perm23(lr);
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) koffA[s] = r * RB + (((2 * s + hh) ^ ((r + 4 * (r >> 3)) & KMASK)) * 16);
+  }
+  int voffT;
+  {
+    const int s16 = lane & 15, g = lane >> 4;
+    const int row = 8 * (g >> 1) + (s16 >> 2);
+    const int chunk = 2 * (g & 1) + ((s16 & 3) >> 1);
+    voffT = row * RB + ((chunk ^ (row & 3)) * 16) + (s16 & 1) * 8;
+  }
+
+  KvWalk walk;
+  walk.bn = BN;
+  walk.mblk = P.mblk_kv;
+  walk.sub = P.mblk_kv / BN;
+  walk.nblk = P.n_kvblk;
+  walk.dense = !P.has_tables;
+  walk.ntiles_dense = (P.Skv + BN - 1) / BN;
+  walk.dense_masked = P.has_mask;
+  walk.full = walk.part = nullptr;
+  walk.nfull = walk.npart = 0;
+  if (P.has_tables) {
+    const int row = tab_row(P, b, h, q0 / P.mblk_q, P.n_qblk);
+    if (P.full_kv_num) {
+      walk.nfull = clamp_count(P.full_kv_num[row], P.kv_width);
+      walk.full = P.full_kv_idx + (size_t)row * P.kv_width;
+    }
+    if (P.kv_num) {
+      walk.npart = clamp_count(P.kv_num[row], P.kv_width);
+      walk.part = P.kv_idx + (size_t)row * P.kv_width;
+    }
+  }
+  const int n_it = walk.count();
+
+  // issue the HBM -> LDS copies of tile `it` into buffer `buf`
+  auto issue = [&](int it, int buf) {
+    int kb;
+    bool msk;
+    walk.get(it, &kb, &msk);
+    kb = kb < P.Skv ? kb : P.Skv;
+    const uint32_t range = (uint32_t)(P.Skv - kb) * RB;
+    const i32x4 rk = make_rsrc(kbase_ptr + (size_t)kb * RB, range);
+    const i32x4 rv = make_rsrc(vbase_ptr + (size_t)kb * RB, range);
+    char* kl = lds + buf * TILE;
+    char* vl = lds + (2 + buf) * TILE;
+#pragma unroll
+    for (int u = 0; u < IPW; ++u) {
+      dma16(rk, dma_off_k[u], kl + (w * IPW + u) * 1024);
+      dma16(rv, dma_off_v[u], vl + (w * IPW + u) * 1024);
+    }
+  };
+
+  f32x16 oacc[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) oacc[i][e] = 0.f;
+  float m = -INFINITY, l = 0.f;  // running max in log2 units, per-lane partial sum
+
+  if (n_it > 0) {
+    issue(0, 0);
+    wait_vmem();
+  }
+  __syncthreads();
+  for (int it = 0; it < n_it; ++it) {
+    const int buf = it & 1;
+    if (it + 1 < n_it) issue(it + 1, buf ^ 1);
+    int kbase;
+    bool masked;
+    walk.get(it, &kbase, &masked);
+    if (kbase < P.Skv) {  // workgroup-uniform
+      masked = masked || (kbase + BN > P.Skv);
+      const char* kl = lds + buf * TILE;
+      const char* vl = lds + (2 + buf) * TILE;
+
+      f32x16 sacc[NSUB];
+#pragma unroll
+      for (int j = 0; j < NSUB; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sacc[j][e] = 0.f;
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+        for (int j = 0; j < NSUB; ++j) {
+          const frag kf = *reinterpret_cast<const u32x4*>(kl + j * 32 * RB + koffA[s]);
+          sacc[j] = E::mma(kf, qf[s], sacc[j]);
+        }
+
+      // logits in log2 units: t = log2(e) * score
+      float mx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < NSUB; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          float t;
+          const int key = kbase + 32 * j + acc_row(e, hh);
+          if constexpr (kMods) {
+            t = score_t<true>(P, sacc[j][e], slope, qw, key, nullptr);
+          } else {
+            t = sacc[j][e] * P.scale_log2;
+          }
+          if (masked && !(key < P.Skv && mask_ok(P, qw, key, qdoc, kv_doc_of(P, b, key)))) t = -INFINITY;
+          sacc[j][e] = t;
+          mx = fmaxf(mx, t);
+        }
+      mx = fmaxf(mx, xor32(mx));
+      const float mnew = fmaxf(m, mx);
+      if (__any(mnew > m)) {
+        const float alpha = fast_exp2(m - (mnew == -INFINITY ? 0.f : mnew));
+        l *= alpha;
+#pragma unroll
+        for (int i = 0; i < DT; ++i)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) oacc[i][e] *= alpha;
+        m = mnew;
+      }
+      const float muse = m == -INFINITY ? 0.f : m;
+      float rs = 0.f;
+#pragma unroll
+      for (int j = 0; j < NSUB; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const float pv = fast_exp2(sacc[j][e] - muse);
+          sacc[j][e] = pv;
+          rs += pv;
+        }
+      l += rs;
+
+      frag pf[BN / 16];
+#pragma unroll
+      for (int c = 0; c < BN / 16; ++c) {
+        float x[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) x[t] = sacc[c >> 1][8 * (c & 1) + t];
+        pf[c] = E::pack(x);
+      }
+#pragma unroll
+      for (int i = 0; i < DT; ++i)
+#pragma unroll
+        for (int c = 0; c < BN / 16; ++c) {
+          const uint2 lo = lds_read_tr16(vl + voffT + (16 * c) * RB + 64 * i);
+          const uint2 hi = lds_read_tr16(vl + voffT + (16 * c + 4) * RB + 64 * i);
+          const frag vf = u32x4{lo.x, lo.y, hi.x, hi.y};
+          oacc[i] = E::mma(vf, pf[c], oacc[i]);
+        }
+    }
+    wait_vmem();
+    __syncthreads();
+  }
+
+  const float lt = l + xor32(l);
+  const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+  if (qvalid) {
+    uint16_t* op = static_cast<uint16_t*>(a.o) + ((size_t)head * P.Sq + qw) * D;
+#pragma unroll
+    for (int i = 0; i < DT; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d0 = 32 * i + 8 * j + 4 * hh;
+        *reinterpret_cast<u32x2*>(op + d0) =
+            u32x2{pack_bf16x2(oacc[i][4 * j] * inv, oacc[i][4 * j + 1] * inv),
+                  pack_bf16x2(oacc[i][4 * j + 2] * inv, oacc[i][4 * j + 3] * inv)};
+      }
+    if (hh == 0) a.lse[(size_t)head * P.Sq + qw] = lt > 0.f ? (m + log2f(lt)) * kLn2 : -INFINITY;
+  }
+}
+
+}  // namespace fa
