@@ -79,6 +79,12 @@ typedef struct fa_params {
   int32_t window_left, window_right;
   const int32_t *q_doc_ids;  /* (B, Sq) or NULL */
   const int32_t *kv_doc_ids; /* (B, Skv) or NULL (required iff q_doc_ids) */
+  /* Optional, with q_doc_ids: documents are contiguous runs of one shared
+   * sequence (self-attention, Sq == Skv) and token t's document spans
+   * [doc_start[b][t], doc_end[b][t]).  Lets the kernels test masks as
+   * intervals instead of comparing ids.  (B, Sq) each, or NULL. */
+  const int32_t *doc_start;
+  const int32_t *doc_end;
   const float *alibi_slopes; /* (Hq) or NULL */
   float softcap;             /* 0 = off */
   int32_t mask_block_q, mask_block_kv;

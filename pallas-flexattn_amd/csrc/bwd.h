@@ -67,9 +67,9 @@ struct QWalk {
   bool dense;
   __device__ __forceinline__ void head_lists(int hq, int* nf, const int** fl, int* np, const int** pl) const {
     const int row = tab_row(*P, b, hq, kvrow, P->n_kvblk);
-    *nf = P->full_q_num ? clamp_count(P->full_q_num[row], P->q_width) : 0;
+    *nf = P->full_q_num ? clamp_count(scalar_load(P->full_q_num, row), P->q_width) : 0;
     *fl = P->full_q_num ? P->full_q_idx + (size_t)row * P->q_width : nullptr;
-    *np = P->q_num ? clamp_count(P->q_num[row], P->q_width) : 0;
+    *np = P->q_num ? clamp_count(scalar_load(P->q_num, row), P->q_width) : 0;
     *pl = P->q_num ? P->q_idx + (size_t)row * P->q_width : nullptr;
   }
   __device__ __forceinline__ int per_head(int hq) const {
@@ -109,7 +109,7 @@ struct QWalk {
     const int *fl, *pl;
     head_lists(*hq, &nf, &fl, &np, &pl);
     const int bi = rem / sub, s = rem - bi * sub;
-    const int idx = bi < nf ? fl[bi] : pl[bi - nf];
+    const int idx = bi < nf ? scalar_load(fl, bi) : scalar_load(pl, bi - nf);
     *masked = bi >= nf;
     *qbase = (idx < 0 || idx >= P->n_qblk) ? kPastEnd : idx * P->mblk_q + s * bq;
   }
@@ -393,11 +393,11 @@ __global__ __launch_bounds__(NW * 64) void dq_kernel(BwdArgs a) {
   if (P.has_tables) {
     const int row = tab_row(P, b, h, q0 / P.mblk_q, P.n_qblk);
     if (P.full_kv_num) {
-      walk.nfull = clamp_count(P.full_kv_num[row], P.kv_width);
+      walk.nfull = clamp_count(scalar_load(P.full_kv_num, row), P.kv_width);
       walk.full = P.full_kv_idx + (size_t)row * P.kv_width;
     }
     if (P.kv_num) {
-      walk.npart = clamp_count(P.kv_num[row], P.kv_width);
+      walk.npart = clamp_count(scalar_load(P.kv_num, row), P.kv_width);
       walk.part = P.kv_idx + (size_t)row * P.kv_width;
     }
   }

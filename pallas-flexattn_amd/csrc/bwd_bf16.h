@@ -1,0 +1,422 @@
+// bf16 backward FlexAttention kernels for gfx950 (the main backward path).
+//
+// Both kernels stage row-major tiles (rows = keys or queries, D bf16 per row)
+// in LDS with buffer_load ... lds, double-buffered one tile ahead, and read
+// them two ways:
+//   * as MFMA A operands "row r, eight consecutive d" (ds_read_b128, rows in
+//     perm23 order so the fp32 results feed the next MFMA from registers);
+//   * transposed, "column d, eight consecutive rows" (two ds_read_b64_tr_b16),
+//     for the products that contract over the tile's rows (K^T in dQ, Q^T and
+//     dO^T in dK/dV) — no transposed copy is ever written.
+// Chunk c (16 bytes) of row r sits in slot c ^ ((r + 4*(r>>3)) & 7), which keeps
+// both access patterns free of bank conflicts.
+//
+//   dq_bf16_kernel   (batch, q head, 32*NW queries): Q, dO rows in VGPRs;
+//                    S^T = K Q^T, dP^T = V dO^T, dS^T = P^T (dP^T - Delta),
+//                    dQ^T += K^T dS^T over the kv-side block tables.
+//   dkdv_bf16_kernel (batch, kv head, 32*NW keys): K, V rows in VGPRs;
+//                    S = Q K^T, dP = dO V^T, dV^T += dO^T P, dK^T += Q^T dS
+//                    over the q-side tables of every q head of the GQA group.
+#pragma once
+#include "bwd.h"
+#include "dma.h"
+
+namespace fa {
+
+// Lane-constant LDS offsets for reading a swizzled row-major bf16 tile.
+template <int D>
+struct RowTile {
+  static constexpr int RB = D * 2;
+  static constexpr int KCH = D / 8;
+  static constexpr int KSTEPS = D / 16;
+  static constexpr int MASK = (KCH >= 8 ? 8 : KCH) - 1;
+  __device__ static __forceinline__ int swz(int r) { return (r + 4 * (r >> 3)) & MASK; }
+
+  int aoff[KSTEPS];  // A operand, rows perm23(lane%32) (+32j), k step s
+  int tr[2][2];      // transposing read: [rows +0..3 / +4..7][d-tile parity]
+
+  __device__ __forceinline__ void init(int lane) {
+    const int lr = lane & 31, hh = lane >> 5;
+    const int r = perm23(lr);
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) aoff[s] = r * RB + (((2 * s + hh) ^ swz(r)) * 16);
+    const int s16 = lane & 15, g = lane >> 4;
+    const int rowbase = 8 * (g >> 1) + (s16 >> 2);
+    const int x = 2 * (g & 1) + ((s16 & 3) >> 1);
+#pragma unroll
+    for (int rd = 0; rd < 2; ++rd) {
+      const int row = 4 * rd + rowbase;
+      const int z = swz(row);
+      const int base = row * RB + ((x ^ (z & 3)) * 16) + (s16 & 1) * 8;
+      const int zb = (z >> 2) * 64;
+      tr[rd][0] = base + zb;  // even d tiles: chunk 4*dt + ... with bit 2 flipped by zb
+      tr[rd][1] = base - zb;  // odd d tiles
+    }
+  }
+  // A operand: rows 32*j + perm23(lane%32), d = 16*s + 8*(lane/32) + [0..7]
+  __device__ __forceinline__ u32x4 a_frag(const char* tile, int j, int s) const {
+    return *reinterpret_cast<const u32x4*>(tile + j * 32 * RB + aoff[s]);
+  }
+  // transposed A operand: row d = 32*dt + lane%32, k = tile rows 16*c + 8*(lane/32) + [0..7]
+  __device__ __forceinline__ u32x4 t_frag(const char* tile, int dt, int c) const {
+    const uint2 lo = lds_read_tr16(tile + tr[0][dt & 1] + 16 * c * RB + 64 * dt);
+    const uint2 hi = lds_read_tr16(tile + tr[1][dt & 1] + 16 * c * RB + 64 * dt);
+    return u32x4{lo.x, lo.y, hi.x, hi.y};
+  }
+};
+
+// per-lane DMA source offsets for copying an R-row tile with NW waves
+template <int D, int R, int NW>
+struct TileDma {
+  static constexpr int RB = D * 2;
+  static constexpr int KCH = D / 8;
+  static constexpr int IPW = R * RB / 1024 / NW;
+  static_assert((R * RB) % (1024 * NW) == 0, "DMA split");
+  int off[IPW];
+  __device__ __forceinline__ void init(int lane, int w) {
+#pragma unroll
+    for (int u = 0; u < IPW; ++u) {
+      const int g = (w * IPW + u) * 64 + lane;
+      const int r = g / KCH, p = g % KCH;
+      off[u] = r * RB + ((p ^ RowTile<D>::swz(r)) * 16);
+    }
+  }
+  // rows [row0, row0 + R) of a tensor with `rows` rows starting at `base`
+  __device__ __forceinline__ void issue(const char* base, int row0, int rows, char* lds_tile, int w) const {
+    row0 = row0 < rows ? row0 : rows;
+    const i32x4 rs = make_rsrc(base + (size_t)row0 * RB, (uint32_t)(rows - row0) * RB);
+#pragma unroll
+    for (int u = 0; u < IPW; ++u) dma16(rs, off[u], lds_tile + (w * IPW + u) * 1024);
+  }
+};
+
+// ------------------------------------------------------------------- dQ ----
+template <int D, int BN, int NW, bool kMods>
+__global__ __launch_bounds__(NW * 64) void dq_bf16_kernel(BwdArgs a) {
+  using E = Elt<uint16_t>;
+  using frag = E::frag;
+  constexpr int BM = 32 * NW;
+  constexpr int RB = D * 2;
+  constexpr int KSTEPS = D / 16;
+  constexpr int NSUB = BN / 32;
+  constexpr int DT = D / 32;
+  constexpr int TILE = BN * RB;
+  __shared__ __attribute__((aligned(1024))) char lds[4 * TILE];  // K0 K1 V0 V1
+
+  const Problem& P = a.p;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int lr = lane & 31, hh = lane >> 5;
+  const int nqt = (P.Sq + BM - 1) / BM;
+  int head, qt;
+  work_item(blockIdx.x, P.B * P.Hq, nqt, P.xcd_remap, &head, &qt);
+  const int b = head / P.Hq, h = head - b * P.Hq;
+  const int hk = h / (P.Hq / P.Hkv);
+  const int q0 = qt * BM;
+  const int qw = q0 + 32 * w + lr;
+  const bool qvalid = qw < P.Sq;
+
+  frag qf[KSTEPS], df[KSTEPS];
+  {
+    const i32x4 rq = make_rsrc(static_cast<const char*>(a.q) + (size_t)head * P.Sq * RB, (uint32_t)P.Sq * RB);
+    const i32x4 rd = make_rsrc(static_cast<const char*>(a.dout) + (size_t)head * P.Sq * RB, (uint32_t)P.Sq * RB);
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+      qf[s] = buf_load16(rq, qw * RB + (2 * s + hh) * 16);
+      df[s] = buf_load16(rd, qw * RB + (2 * s + hh) * 16);
+    }
+  }
+  const size_t rowi = (size_t)head * P.Sq + qw;
+  const float lse2 = qvalid ? a.lse[rowi] * kLog2e : INFINITY;
+  const float dl = qvalid ? a.delta[rowi] : 0.f;
+  const float slope = P.alibi ? P.alibi[h] : 0.f;
+  const int qdoc = (P.q_doc && qvalid) ? P.q_doc[(size_t)b * P.Sq + qw] : 0;
+
+  const char* kbase_ptr = static_cast<const char*>(a.k) + (size_t)(b * P.Hkv + hk) * P.Skv * RB;
+  const char* vbase_ptr = static_cast<const char*>(a.v) + (size_t)(b * P.Hkv + hk) * P.Skv * RB;
+  RowTile<D> rt;
+  rt.init(lane);
+  TileDma<D, BN, NW> dma;
+  dma.init(lane, w);
+
+  KvWalk walk;
+  walk.bn = BN;
+  walk.mblk = P.mblk_kv;
+  walk.sub = P.mblk_kv / BN;
+  walk.nblk = P.n_kvblk;
+  walk.dense = !P.has_tables;
+  walk.ntiles_dense = (P.Skv + BN - 1) / BN;
+  walk.dense_masked = P.has_mask;
+  walk.full = walk.part = nullptr;
+  walk.nfull = walk.npart = 0;
+  if (P.has_tables) {
+    const int row = tab_row(P, b, h, q0 / P.mblk_q, P.n_qblk);
+    if (P.full_kv_num) {
+      walk.nfull = clamp_count(scalar_load(P.full_kv_num, row), P.kv_width);
+      walk.full = P.full_kv_idx + (size_t)row * P.kv_width;
+    }
+    if (P.kv_num) {
+      walk.npart = clamp_count(scalar_load(P.kv_num, row), P.kv_width);
+      walk.part = P.kv_idx + (size_t)row * P.kv_width;
+    }
+  }
+  const int n_it = walk.count();
+  auto issue = [&](int it, int buf) {
+    int kb;
+    bool msk;
+    walk.get(it, &kb, &msk);
+    dma.issue(kbase_ptr, kb, P.Skv, lds + buf * TILE, w);
+    dma.issue(vbase_ptr, kb, P.Skv, lds + (2 + buf) * TILE, w);
+  };
+
+  f32x16 dqa[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dqa[i][e] = 0.f;
+
+  if (n_it > 0) {
+    issue(0, 0);
+    wait_vmem();
+  }
+  __syncthreads();
+  for (int it = 0; it < n_it; ++it) {
+    const int buf = it & 1;
+    if (it + 1 < n_it) issue(it + 1, buf ^ 1);
+    int kbase;
+    bool masked;
+    walk.get(it, &kbase, &masked);
+    if (kbase < P.Skv) {
+      masked = masked || (kbase + BN > P.Skv);
+      const char* kl = lds + buf * TILE;
+      const char* vl = lds + (2 + buf) * TILE;
+      f32x16 sacc[NSUB], pacc[NSUB];
+#pragma unroll
+      for (int j = 0; j < NSUB; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sacc[j][e] = pacc[j][e] = 0.f;
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+        for (int j = 0; j < NSUB; ++j) {
+          sacc[j] = E::mma(rt.a_frag(kl, j, s), qf[s], sacc[j]);
+          pacc[j] = E::mma(rt.a_frag(vl, j, s), df[s], pacc[j]);
+        }
+#pragma unroll
+      for (int j = 0; j < NSUB; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int key = kbase + 32 * j + acc_row(e, hh);
+          float dsdx = 1.f;
+          float t;
+          if constexpr (kMods) t = score_t<true>(P, sacc[j][e], slope, qw, key, &dsdx);
+          else t = sacc[j][e] * P.scale_log2;
+          if (masked && !(key < P.Skv && mask_ok(P, qw, key, qdoc, kv_doc_of(P, b, key)))) t = -INFINITY;
+          const float pv = fast_exp2(t - lse2);
+          if constexpr (kMods) pacc[j][e] = pv * (pacc[j][e] - dl) * dsdx;
+          else pacc[j][e] = pv * (pacc[j][e] - dl);
+        }
+      frag sf[BN / 16];
+#pragma unroll
+      for (int c = 0; c < BN / 16; ++c) {
+        float y[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) y[t] = pacc[c >> 1][8 * (c & 1) + t];
+        sf[c] = E::pack(y);
+      }
+#pragma unroll
+      for (int i = 0; i < DT; ++i)
+#pragma unroll
+        for (int c = 0; c < BN / 16; ++c) dqa[i] = E::mma(rt.t_frag(kl, i, c), sf[c], dqa[i]);
+    }
+    wait_vmem();
+    __syncthreads();
+  }
+
+  if (qvalid) {
+    uint16_t* dqp = static_cast<uint16_t*>(a.dq) + rowi * D;
+#pragma unroll
+    for (int i = 0; i < DT; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d0 = 32 * i + 8 * j + 4 * hh;
+        *reinterpret_cast<u32x2*>(dqp + d0) =
+            u32x2{pack_bf16x2(dqa[i][4 * j] * P.scale, dqa[i][4 * j + 1] * P.scale),
+                  pack_bf16x2(dqa[i][4 * j + 2] * P.scale, dqa[i][4 * j + 3] * P.scale)};
+      }
+  }
+}
+
+// ---------------------------------------------------------------- dK dV ----
+template <int D, int BQ, int NW, bool kMods>
+__global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
+  using E = Elt<uint16_t>;
+  using frag = E::frag;
+  constexpr int BKV = 32 * NW;
+  constexpr int RB = D * 2;
+  constexpr int KSTEPS = D / 16;
+  constexpr int NQS = BQ / 32;
+  constexpr int DT = D / 32;
+  constexpr int TILE = BQ * RB;
+  constexpr int STAT = 1024;  // LSE / Delta landing zone per buffer (BQ floats used)
+  static_assert(BQ * 4 <= STAT, "stat tile");
+  __shared__ __attribute__((aligned(1024))) char lds[4 * TILE + 4 * STAT];  // Q0 Q1 dO0 dO1 L0 L1 D0 D1
+
+  const Problem& P = a.p;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int lr = lane & 31, hh = lane >> 5;
+  const int nkt = (P.Skv + BKV - 1) / BKV;
+  const int g = P.Hq / P.Hkv;
+  int head, kt;
+  work_item(blockIdx.x, P.B * P.Hkv, nkt, P.xcd_remap, &head, &kt);
+  const int b = head / P.Hkv, hk = head - b * P.Hkv;
+  const int k0 = kt * BKV;
+  const int kw = k0 + 32 * w + lr;
+  const bool kvalid = kw < P.Skv;
+
+  frag kf[KSTEPS], vf[KSTEPS];
+  {
+    const i32x4 rk = make_rsrc(static_cast<const char*>(a.k) + (size_t)head * P.Skv * RB, (uint32_t)P.Skv * RB);
+    const i32x4 rv = make_rsrc(static_cast<const char*>(a.v) + (size_t)head * P.Skv * RB, (uint32_t)P.Skv * RB);
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+      kf[s] = buf_load16(rk, kw * RB + (2 * s + hh) * 16);
+      vf[s] = buf_load16(rv, kw * RB + (2 * s + hh) * 16);
+    }
+  }
+  const int kdoc = (P.q_doc && kvalid) ? P.kv_doc[(size_t)b * P.Skv + kw] : 0;
+
+  RowTile<D> rt;
+  rt.init(lane);
+  TileDma<D, BQ, NW> dma;
+  dma.init(lane, w);
+
+  QWalk walk;
+  walk.P = &P;
+  walk.b = b;
+  walk.hq0 = hk * g;
+  walk.g = g;
+  walk.kvrow = k0 / P.mblk_kv;
+  walk.sub = P.mblk_q / BQ;
+  walk.bq = BQ;
+  walk.dense = !P.has_tables;
+  walk.ntiles_dense = (P.Sq + BQ - 1) / BQ;
+  const int n_it = walk.count();
+
+  auto issue = [&](int it, int buf) {
+    int hq, qb;
+    bool msk;
+    walk.get(it, &hq, &qb, &msk);
+    const size_t hoff = (size_t)(b * P.Hq + hq) * P.Sq;
+    dma.issue(static_cast<const char*>(a.q) + hoff * RB, qb, P.Sq, lds + buf * TILE, w);
+    dma.issue(static_cast<const char*>(a.dout) + hoff * RB, qb, P.Sq, lds + (2 + buf) * TILE, w);
+    if (w == 0) {
+      const int q = qb < P.Sq ? qb : P.Sq;
+      const uint32_t range = (uint32_t)(P.Sq - q) * 4;
+      const i32x4 rl = make_rsrc(a.lse + hoff + q, range);
+      const i32x4 rdl = make_rsrc(a.delta + hoff + q, range);
+      dma16(rl, lane * 16, lds + 4 * TILE + buf * STAT);
+      dma16(rdl, lane * 16, lds + 4 * TILE + (2 + buf) * STAT);
+    }
+  };
+
+  f32x16 dka[DT], dva[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dka[i][e] = dva[i][e] = 0.f;
+
+  if (n_it > 0) {
+    issue(0, 0);
+    wait_vmem();
+  }
+  __syncthreads();
+  for (int it = 0; it < n_it; ++it) {
+    const int buf = it & 1;
+    if (it + 1 < n_it) issue(it + 1, buf ^ 1);
+    int hq, qbase;
+    bool masked;
+    walk.get(it, &hq, &qbase, &masked);
+    if (qbase < P.Sq) {
+      masked = masked || (k0 + BKV > P.Skv) || (qbase + BQ > P.Sq);
+      const float slope = P.alibi ? P.alibi[hq] : 0.f;
+      const char* ql = lds + buf * TILE;
+      const char* dl_ = lds + (2 + buf) * TILE;
+      const float* lsel = reinterpret_cast<const float*>(lds + 4 * TILE + buf * STAT);
+      const float* dltl = reinterpret_cast<const float*>(lds + 4 * TILE + (2 + buf) * STAT);
+
+      f32x16 sacc[NQS], pacc[NQS];
+#pragma unroll
+      for (int j = 0; j < NQS; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sacc[j][e] = pacc[j][e] = 0.f;
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+        for (int j = 0; j < NQS; ++j) {
+          sacc[j] = E::mma(rt.a_frag(ql, j, s), kf[s], sacc[j]);
+          pacc[j] = E::mma(rt.a_frag(dl_, j, s), vf[s], pacc[j]);
+        }
+#pragma unroll
+      for (int j = 0; j < NQS; ++j)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+          const int r0 = 32 * j + acc_row(4 * e4, hh);
+          const f32x4 ls = *reinterpret_cast<const f32x4*>(lsel + r0);
+          const f32x4 dt4 = *reinterpret_cast<const f32x4*>(dltl + r0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int e = 4 * e4 + i;
+            const int qi = qbase + r0 + i;
+            float dsdx = 1.f;
+            float t;
+            if constexpr (kMods) t = score_t<true>(P, sacc[j][e], slope, qi, kw, &dsdx);
+            else t = sacc[j][e] * P.scale_log2;
+            if (masked && !(kvalid && qi < P.Sq && mask_ok(P, qi, kw, q_doc_of(P, b, qi), kdoc))) t = -INFINITY;
+            const float pv = fast_exp2(t - ls[i] * kLog2e);
+            sacc[j][e] = pv;
+            if constexpr (kMods) pacc[j][e] = pv * (pacc[j][e] - dt4[i]) * dsdx;
+            else pacc[j][e] = pv * (pacc[j][e] - dt4[i]);
+          }
+        }
+      frag pf[BQ / 16], sf[BQ / 16];
+#pragma unroll
+      for (int c = 0; c < BQ / 16; ++c) {
+        float x[8], y[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          x[t] = sacc[c >> 1][8 * (c & 1) + t];
+          y[t] = pacc[c >> 1][8 * (c & 1) + t];
+        }
+        pf[c] = E::pack(x);
+        sf[c] = E::pack(y);
+      }
+#pragma unroll
+      for (int i = 0; i < DT; ++i)
+#pragma unroll
+        for (int c = 0; c < BQ / 16; ++c) {
+          dva[i] = E::mma(rt.t_frag(dl_, i, c), pf[c], dva[i]);
+          dka[i] = E::mma(rt.t_frag(ql, i, c), sf[c], dka[i]);
+        }
+    }
+    wait_vmem();
+    __syncthreads();
+  }
+
+  if (kvalid) {
+    uint16_t* dkp = static_cast<uint16_t*>(a.dk) + ((size_t)head * P.Skv + kw) * D;
+    uint16_t* dvp = static_cast<uint16_t*>(a.dv) + ((size_t)head * P.Skv + kw) * D;
+#pragma unroll
+    for (int i = 0; i < DT; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d0 = 32 * i + 8 * j + 4 * hh;
+        *reinterpret_cast<u32x2*>(dkp + d0) =
+            u32x2{pack_bf16x2(dka[i][4 * j] * P.scale, dka[i][4 * j + 1] * P.scale),
+                  pack_bf16x2(dka[i][4 * j + 2] * P.scale, dka[i][4 * j + 3] * P.scale)};
+        *reinterpret_cast<u32x2*>(dvp + d0) = u32x2{pack_bf16x2(dva[i][4 * j], dva[i][4 * j + 1]),
+                                                    pack_bf16x2(dva[i][4 * j + 2], dva[i][4 * j + 3])};
+      }
+  }
+}
+
+}  // namespace fa

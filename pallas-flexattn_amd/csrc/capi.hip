@@ -4,6 +4,7 @@
 
 #include "../../include/flexattn.h"
 #include "bwd.h"
+#include "bwd_bf16.h"
 #include "fwd_bf16.h"
 
 namespace {
@@ -57,6 +58,10 @@ int build_problem(const fa_params* p, const Tiles& t, Problem* pr) {
   r.win_right = p->window_right < 0 ? -1 : p->window_right;
   r.q_doc = p->q_doc_ids;
   r.kv_doc = p->kv_doc_ids;
+  if ((p->doc_start == nullptr) != (p->doc_end == nullptr)) return FA_ERR_NULL;
+  if (p->doc_start && (!p->q_doc_ids || p->Sq != p->Skv)) return FA_ERR_SHAPE;
+  r.doc_start = p->doc_start;
+  r.doc_end = p->doc_end;
   r.alibi = p->alibi_slopes;
   r.softcap = p->softcap;
   r.has_mask = (r.win_left >= 0 || r.win_right >= 0 || r.q_doc != nullptr) ? 1 : 0;
@@ -129,14 +134,22 @@ bool has_mods(const Problem& p) { return p.alibi != nullptr || p.softcap > 0.f; 
 template <typename T, int D, int BN, int NW, bool M>
 int run_dq(const BwdArgs& a, hipStream_t s) {
   const int grid = a.p.B * a.p.Hq * cdiv(a.p.Sq, 32 * NW);
-  hipLaunchKernelGGL((fa::dq_kernel<T, D, BN, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
+  if constexpr (sizeof(T) == 2) {
+    hipLaunchKernelGGL((fa::dq_bf16_kernel<D, BN, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((fa::dq_kernel<T, D, BN, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
+  }
   return launch_status();
 }
 
 template <typename T, int D, int BQ, int NW, bool M>
 int run_dkdv(const BwdArgs& a, hipStream_t s) {
   const int grid = a.p.B * a.p.Hkv * cdiv(a.p.Skv, 32 * NW);
-  hipLaunchKernelGGL((fa::dkdv_kernel<T, D, BQ, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
+  if constexpr (sizeof(T) == 2) {
+    hipLaunchKernelGGL((fa::dkdv_bf16_kernel<D, BQ, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((fa::dkdv_kernel<T, D, BQ, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
+  }
   return launch_status();
 }
 

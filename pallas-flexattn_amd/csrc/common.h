@@ -50,6 +50,30 @@ __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w 
 
 __device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32, 64); }
 
+// v_permlane32_swap(x, x) yields {x[l % 32], x[l % 32 + 32]} in every lane l,
+// so reductions over the lane pair (l, l ^ 32) need no LDS traffic.
+__device__ __forceinline__ float pair_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Load through the scalar data cache (the address must be wave-uniform).
+__device__ __forceinline__ int scalar_load(const int* p, int i) {
+  typedef const __attribute__((address_space(4))) int* cptr;
+  return ((cptr)(p))[i];
+}
+
+// Scheduling hints (llvm.amdgcn.sched.group.barrier masks).
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedVmemRead = 0x020;
+constexpr int kSchedDsRead = 0x100;
+constexpr int kSchedDsWrite = 0x200;
+constexpr int kSchedValu = 0x002;
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 

@@ -40,7 +40,7 @@ struct KvWalk {
       return;
     }
     const int bi = it / sub, s = it - bi * sub;
-    const int idx = bi < nfull ? full[bi] : part[bi - nfull];
+    const int idx = bi < nfull ? scalar_load(full, bi) : scalar_load(part, bi - nfull);
     *masked = bi >= nfull;
     // an out-of-range table entry becomes a tile past the end (skipped)
     *kbase = (idx < 0 || idx >= nblk) ? kPastEnd : idx * mblk + s * bn;
@@ -105,11 +105,11 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdArgs a) {
   if (P.has_tables) {
     const int row = tab_row(P, b, h, q0 / P.mblk_q, P.n_qblk);
     if (P.full_kv_num) {
-      walk.nfull = clamp_count(P.full_kv_num[row], P.kv_width);
+      walk.nfull = clamp_count(scalar_load(P.full_kv_num, row), P.kv_width);
       walk.full = P.full_kv_idx + (size_t)row * P.kv_width;
     }
     if (P.kv_num) {
-      walk.npart = clamp_count(P.kv_num[row], P.kv_width);
+      walk.npart = clamp_count(scalar_load(P.kv_num, row), P.kv_width);
       walk.part = P.kv_idx + (size_t)row * P.kv_width;
     }
   }

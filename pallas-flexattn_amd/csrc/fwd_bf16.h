@@ -6,12 +6,15 @@
 // Per kv tile of BN keys (double-buffered in LDS, one barrier per tile):
 //   * K and V tiles are copied HBM -> LDS with buffer_load ... lds (no
 //     registers, no bounds branches: rows past the sequence read as zero),
-//     issued one tile ahead;
-//   * S^T = K Q^T   (A = K rows from LDS in perm23 order, B = Q from VGPRs);
+//     issued one tile ahead; block-table entries come through the scalar cache;
+//   * S^T = K Q^T   (A = K rows from LDS in perm23 order, fetched one k-step
+//     ahead of the MFMAs; B = Q from VGPRs);
 //   * online softmax with one query per lane: row max / sum are per-lane
-//     scalars plus one exchange between lane halves; O is rescaled only when
-//     some row maximum grew (multiplying by exp2(0) = 1 is skipped, so results
-//     are unchanged);
+//     scalars plus a v_permlane32_swap between lane halves; O is rescaled only
+//     when some row maximum grew (multiplying by exp2(0) = 1 is skipped, so
+//     results are unchanged); fully-live tiles skip the element mask, partial
+//     tiles test key in [lo, hi] (window and contiguous documents are
+//     intervals per query) or compare document ids;
 //   * O^T += V^T P^T (A = V^T fetched from the row-major V tile with
 //     ds_read_b64_tr_b16, B = P^T straight from the S^T accumulators).
 // LDS layouts (row = key, 16-byte chunks): K chunk c of row r sits in slot
@@ -19,6 +22,8 @@
 // land in distinct banks; V chunk c sits in slot c ^ (r & 3) — the 4
 // consecutive rows of one transposing read land in distinct banks.
 #pragma once
+#include <type_traits>
+
 #include "dma.h"
 #include "fwd.h"
 
@@ -66,15 +71,17 @@ void fwd_bf16_kernel(FwdArgs a) {
     for (int s = 0; s < KSTEPS; ++s) qf[s] = buf_load16(rq, qw * RB + (2 * s + hh) * 16);
   }
   const float slope = P.alibi ? P.alibi[h] : 0.f;
+  const bool by_interval = interval_mask(P);
+  int klo, khi;
+  key_interval(P, b, qw, &klo, &khi);
   const int qdoc = (P.q_doc && qvalid) ? P.q_doc[(size_t)b * P.Sq + qw] : 0;
 
   // loop-invariant LDS / global offsets
-  int dma_off_k[IPW], dma_off_v[IPW], dma_row[IPW];
+  int dma_off_k[IPW], dma_off_v[IPW];
 #pragma unroll
   for (int u = 0; u < IPW; ++u) {
     const int g = (w * IPW + u) * 64 + lane;
     const int r = g / KCH, p = g % KCH;
-    dma_row[u] = r;
     dma_off_k[u] = r * RB + ((p ^ ((r + 4 * (r >> 3)) & KMASK)) * 16);
     dma_off_v[u] = r * RB + ((p ^ (r & 3)) * 16);
   }
@@ -105,21 +112,18 @@ void fwd_bf16_kernel(FwdArgs a) {
   if (P.has_tables) {
     const int row = tab_row(P, b, h, q0 / P.mblk_q, P.n_qblk);
     if (P.full_kv_num) {
-      walk.nfull = clamp_count(P.full_kv_num[row], P.kv_width);
+      walk.nfull = clamp_count(scalar_load(P.full_kv_num, row), P.kv_width);
       walk.full = P.full_kv_idx + (size_t)row * P.kv_width;
     }
     if (P.kv_num) {
-      walk.npart = clamp_count(P.kv_num[row], P.kv_width);
+      walk.npart = clamp_count(scalar_load(P.kv_num, row), P.kv_width);
       walk.part = P.kv_idx + (size_t)row * P.kv_width;
     }
   }
   const int n_it = walk.count();
 
-  // issue the HBM -> LDS copies of tile `it` into buffer `buf`
-  auto issue = [&](int it, int buf) {
-    int kb;
-    bool msk;
-    walk.get(it, &kb, &msk);
+  // HBM -> LDS copies of the tile starting at key kb into buffer `buf`
+  auto issue = [&](int kb, int buf) {
     kb = kb < P.Skv ? kb : P.Skv;
     const uint32_t range = (uint32_t)(P.Skv - kb) * RB;
     const i32x4 rk = make_rsrc(kbase_ptr + (size_t)kb * RB, range);
@@ -140,17 +144,65 @@ void fwd_bf16_kernel(FwdArgs a) {
     for (int e = 0; e < 16; ++e) oacc[i][e] = 0.f;
   float m = -INFINITY, l = 0.f;  // running max in log2 units, per-lane partial sum
 
+  // softmax of one tile held in sacc (log2-domain logits written back as P)
+  auto softmax = [&](f32x16* sacc, int kbase, auto masked_c) {
+    constexpr bool kMasked = decltype(masked_c)::value;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NSUB; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int key = kbase + 32 * j + acc_row(e, hh);
+        float t;
+        if constexpr (kMods) t = score_t<true>(P, sacc[j][e], slope, qw, key, nullptr);
+        else t = sacc[j][e] * P.scale_log2;
+        if constexpr (kMasked) {
+          const bool ok = by_interval ? (key >= klo && key <= khi)
+                                      : (key < P.Skv && window_ok(P, qw, key) && qdoc == kv_doc_of(P, b, key));
+          t = ok ? t : -INFINITY;
+        }
+        sacc[j][e] = t;
+        mx = fmaxf(mx, t);
+      }
+    const float mnew = fmaxf(m, pair_max(mx));
+    if (__any(mnew > m)) {
+      const float alpha = fast_exp2(m - (mnew == -INFINITY ? 0.f : mnew));
+      l *= alpha;
+#pragma unroll
+      for (int i = 0; i < DT; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) oacc[i][e] *= alpha;
+      m = mnew;
+    }
+    const float muse = m == -INFINITY ? 0.f : m;
+    float rs = 0.f;
+#pragma unroll
+    for (int j = 0; j < NSUB; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float pv = fast_exp2(sacc[j][e] - muse);
+        sacc[j][e] = pv;
+        rs += pv;
+      }
+    l += rs;
+  };
+
+  int kb_next = 0;
+  bool msk_next = false;
   if (n_it > 0) {
-    issue(0, 0);
+    walk.get(0, &kb_next, &msk_next);
+    issue(kb_next, 0);
     wait_vmem();
   }
   __syncthreads();
   for (int it = 0; it < n_it; ++it) {
     const int buf = it & 1;
-    if (it + 1 < n_it) issue(it + 1, buf ^ 1);
-    int kbase;
-    bool masked;
-    walk.get(it, &kbase, &masked);
+    const int kbase = kb_next;
+    bool masked = msk_next;
+    if (it + 1 < n_it) {
+      walk.get(it + 1, &kb_next, &msk_next);
+      issue(kb_next, buf ^ 1);
+    }
     if (kbase < P.Skv) {  // workgroup-uniform
       masked = masked || (kbase + BN > P.Skv);
       const char* kl = lds + buf * TILE;
@@ -161,53 +213,22 @@ void fwd_bf16_kernel(FwdArgs a) {
       for (int j = 0; j < NSUB; ++j)
 #pragma unroll
         for (int e = 0; e < 16; ++e) sacc[j][e] = 0.f;
+      frag ka[2][NSUB];
 #pragma unroll
-      for (int s = 0; s < KSTEPS; ++s)
+      for (int j = 0; j < NSUB; ++j) ka[0][j] = *reinterpret_cast<const u32x4*>(kl + j * 32 * RB + koffA[0]);
 #pragma unroll
-        for (int j = 0; j < NSUB; ++j) {
-          const frag kf = *reinterpret_cast<const u32x4*>(kl + j * 32 * RB + koffA[s]);
-          sacc[j] = E::mma(kf, qf[s], sacc[j]);
+      for (int s = 0; s < KSTEPS; ++s) {
+        if (s + 1 < KSTEPS) {
+#pragma unroll
+          for (int j = 0; j < NSUB; ++j)
+            ka[(s + 1) & 1][j] = *reinterpret_cast<const u32x4*>(kl + j * 32 * RB + koffA[s + 1]);
         }
-
-      // logits in log2 units: t = log2(e) * score
-      float mx = -INFINITY;
 #pragma unroll
-      for (int j = 0; j < NSUB; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          float t;
-          const int key = kbase + 32 * j + acc_row(e, hh);
-          if constexpr (kMods) {
-            t = score_t<true>(P, sacc[j][e], slope, qw, key, nullptr);
-          } else {
-            t = sacc[j][e] * P.scale_log2;
-          }
-          if (masked && !(key < P.Skv && mask_ok(P, qw, key, qdoc, kv_doc_of(P, b, key)))) t = -INFINITY;
-          sacc[j][e] = t;
-          mx = fmaxf(mx, t);
-        }
-      mx = fmaxf(mx, xor32(mx));
-      const float mnew = fmaxf(m, mx);
-      if (__any(mnew > m)) {
-        const float alpha = fast_exp2(m - (mnew == -INFINITY ? 0.f : mnew));
-        l *= alpha;
-#pragma unroll
-        for (int i = 0; i < DT; ++i)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) oacc[i][e] *= alpha;
-        m = mnew;
+        for (int j = 0; j < NSUB; ++j) sacc[j] = E::mma(ka[s & 1][j], qf[s], sacc[j]);
       }
-      const float muse = m == -INFINITY ? 0.f : m;
-      float rs = 0.f;
-#pragma unroll
-      for (int j = 0; j < NSUB; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const float pv = fast_exp2(sacc[j][e] - muse);
-          sacc[j][e] = pv;
-          rs += pv;
-        }
-      l += rs;
+
+      if (masked) softmax(sacc, kbase, std::true_type{});
+      else softmax(sacc, kbase, std::false_type{});
 
       frag pf[BN / 16];
 #pragma unroll
@@ -231,7 +252,7 @@ void fwd_bf16_kernel(FwdArgs a) {
     __syncthreads();
   }
 
-  const float lt = l + xor32(l);
+  const float lt = pair_sum(l);
   const float inv = lt > 0.f ? 1.0f / lt : 0.f;
   if (qvalid) {
     uint16_t* op = static_cast<uint16_t*>(a.o) + ((size_t)head * P.Sq + qw) * D;

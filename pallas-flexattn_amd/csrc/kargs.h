@@ -15,6 +15,10 @@ struct Problem {
   int win_left, win_right;
   const int* q_doc;   // (B, Sq) or null
   const int* kv_doc;  // (B, Skv) or null
+  // contiguous documents (self-attention): token t's document is
+  // [doc_start[b][t], doc_end[b][t]); when set, masks are key/query intervals
+  const int* doc_start;
+  const int* doc_end;
   // score modification: s += alibi[h] * (kv - q); then s = cap * tanh(s / cap)
   const float* alibi;  // (Hq) or null
   float softcap;       // <= 0: off
@@ -43,6 +47,37 @@ __device__ __forceinline__ bool window_ok(const Problem& p, int q, int k) {
 // Full element mask given the two document ids (ignored without documents).
 __device__ __forceinline__ bool mask_ok(const Problem& p, int q, int k, int qdoc, int kdoc) {
   return window_ok(p, q, k) && (p.q_doc == nullptr || qdoc == kdoc);
+}
+
+// True when every mask term is an interval on the other sequence (window
+// and/or contiguous documents); false for arbitrary document labels.
+__device__ __forceinline__ bool interval_mask(const Problem& p) {
+  return p.q_doc == nullptr || p.doc_start != nullptr;
+}
+
+// Keys visible to query q: [lo, hi] (empty when lo > hi).  With delta = q - k,
+// delta <= left gives k >= q - left and -delta <= right gives k <= q + right.
+__device__ __forceinline__ void key_interval(const Problem& p, int b, int q, int* lo, int* hi) {
+  int l = p.win_left >= 0 ? q - p.win_left : 0;
+  int h = p.win_right >= 0 ? q + p.win_right : p.Skv - 1;
+  if (p.doc_start != nullptr && q < p.Sq) {
+    l = max(l, p.doc_start[(size_t)b * p.Sq + q]);
+    h = min(h, p.doc_end[(size_t)b * p.Sq + q] - 1);
+  }
+  *lo = max(l, 0);
+  *hi = q < p.Sq ? min(h, p.Skv - 1) : -1;
+}
+
+// Queries that see key k: [lo, hi] (q <= k + left, q >= k - right).
+__device__ __forceinline__ void query_interval(const Problem& p, int b, int k, int* lo, int* hi) {
+  int l = p.win_right >= 0 ? k - p.win_right : 0;
+  int h = p.win_left >= 0 ? k + p.win_left : p.Sq - 1;
+  if (p.doc_start != nullptr && k < p.Skv) {
+    l = max(l, p.doc_start[(size_t)b * p.Skv + k]);
+    h = min(h, p.doc_end[(size_t)b * p.Skv + k] - 1);
+  }
+  *lo = max(l, 0);
+  *hi = k < p.Skv ? min(h, p.Sq - 1) : -1;
 }
 
 __device__ __forceinline__ int kv_doc_of(const Problem& p, int b, int k) {

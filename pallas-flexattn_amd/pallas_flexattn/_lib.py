@@ -27,6 +27,7 @@ class FaParams(ctypes.Structure):
         ("scale", ctypes.c_float),
         ("window_left", _i32), ("window_right", _i32),
         ("q_doc_ids", _pi32), ("kv_doc_ids", _pi32),
+        ("doc_start", _pi32), ("doc_end", _pi32),
         ("alibi_slopes", _pf),
         ("softcap", ctypes.c_float),
         ("mask_block_q", _i32), ("mask_block_kv", _i32),

@@ -109,6 +109,12 @@ class _Plan:
                 tk = torch.from_numpy(dk_).to(dev)
                 self.keep += [tq, tk]
                 p.q_doc_ids, p.kv_doc_ids = tq.data_ptr(), tk.data_ptr()
+                bounds = mask.doc_bounds()
+                if bounds is not None and Sq == Skv and docs.shape[1] == Sq:
+                    ts, te = (torch.from_numpy(np.array(np.broadcast_to(x, (B, Sq)), dtype=np.int32)).to(dev)
+                              for x in bounds)
+                    self.keep += [ts, te]
+                    p.doc_start, p.doc_end = ts.data_ptr(), te.data_ptr()
         if score is not None:
             if score.alibi is not None:
                 if score.alibi.shape[0] != Hq:

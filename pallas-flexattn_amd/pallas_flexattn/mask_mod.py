@@ -70,6 +70,28 @@ class MaskSpec:
 
     head_dependent = False
 
+    def doc_bounds(self):
+        """(start, end) int32 arrays shaped like ``doc_ids``: token t's document
+        spans [start[t], end[t]).  None unless every document is one contiguous
+        run in every row (then masks are intervals for the kernels)."""
+        if self.doc_ids is None:
+            return None
+        if not hasattr(self, "_bounds"):
+            starts, ends = [], []
+            ok = True
+            for row in self.doc_ids:
+                change = np.flatnonzero(np.diff(row)) + 1
+                s = np.concatenate([[0], change])
+                e = np.concatenate([change, [len(row)]])
+                if len(np.unique(row[s])) != len(s):
+                    ok = False
+                    break
+                run = np.repeat(np.arange(len(s)), e - s)
+                starts.append(s[run].astype(np.int32))
+                ends.append(e[run].astype(np.int32))
+            self._bounds = (np.stack(starts), np.stack(ends)) if ok else None
+        return self._bounds
+
     def key(self):
         """Hashable identity (used for caching block masks)."""
         docs = None if self.doc_ids is None else (self.doc_ids.shape, hash(self.doc_ids.tobytes()))
