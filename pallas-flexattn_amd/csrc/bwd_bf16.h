@@ -9,7 +9,8 @@
 //     for the products that contract over the tile's rows (K^T in dQ, Q^T and
 //     dO^T in dK/dV) — no transposed copy is ever written.
 // Chunk c (16 bytes) of row r sits in slot c ^ ((r + 4*(r>>3)) & 7), which keeps
-// both access patterns free of bank conflicts.
+// both access patterns free of bank conflicts.  Every MFMA phase fetches the
+// operands of step k+1 before issuing the MFMAs of step k.
 //
 //   dq_bf16_kernel   (batch, q head, 32*NW queries): Q, dO rows in VGPRs;
 //                    S^T = K Q^T, dP^T = V dO^T, dS^T = P^T (dP^T - Delta),
@@ -17,7 +18,11 @@
 //   dkdv_bf16_kernel (batch, kv head, 32*NW keys): K, V rows in VGPRs;
 //                    S = Q K^T, dP = dO V^T, dV^T += dO^T P, dK^T += Q^T dS
 //                    over the q-side tables of every q head of the GQA group.
+// Partial tiles apply the element mask (an interval per lane for windows and
+// contiguous documents); full tiles skip it.
 #pragma once
+#include <type_traits>
+
 #include "bwd.h"
 #include "dma.h"
 
@@ -49,7 +54,7 @@ struct RowTile {
       const int z = swz(row);
       const int base = row * RB + ((x ^ (z & 3)) * 16) + (s16 & 1) * 8;
       const int zb = (z >> 2) * 64;
-      tr[rd][0] = base + zb;  // even d tiles: chunk 4*dt + ... with bit 2 flipped by zb
+      tr[rd][0] = base + zb;  // even d tiles: bit 2 of the chunk index is flipped by z
       tr[rd][1] = base - zb;  // odd d tiles
     }
   }
@@ -90,6 +95,36 @@ struct TileDma {
   }
 };
 
+// acc[j] += A(tileA rows, j) * bA[s]  and  acc2[j] += A(tileB rows, j) * bB[s]
+// over all k steps, operands fetched one step ahead.
+template <int D, int NJ>
+__device__ __forceinline__ void mma_rows2(const RowTile<D>& rt, const char* ta, const char* tb,
+                                          const u32x4* ba, const u32x4* bb, f32x16* acc, f32x16* acc2) {
+  using E = Elt<uint16_t>;
+  constexpr int KS = D / 16;
+  u32x4 fa[2][NJ], fb[2][NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    fa[0][j] = rt.a_frag(ta, j, 0);
+    fb[0][j] = rt.a_frag(tb, j, 0);
+  }
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    if (s + 1 < KS) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        fa[(s + 1) & 1][j] = rt.a_frag(ta, j, s + 1);
+        fb[(s + 1) & 1][j] = rt.a_frag(tb, j, s + 1);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      acc[j] = E::mma(fa[s & 1][j], ba[s], acc[j]);
+      acc2[j] = E::mma(fb[s & 1][j], bb[s], acc2[j]);
+    }
+  }
+}
+
 // ------------------------------------------------------------------- dQ ----
 template <int D, int BN, int NW, bool kMods>
 __global__ __launch_bounds__(NW * 64) void dq_bf16_kernel(BwdArgs a) {
@@ -100,6 +135,7 @@ __global__ __launch_bounds__(NW * 64) void dq_bf16_kernel(BwdArgs a) {
   constexpr int KSTEPS = D / 16;
   constexpr int NSUB = BN / 32;
   constexpr int DT = D / 32;
+  constexpr int NC = BN / 16;
   constexpr int TILE = BN * RB;
   __shared__ __attribute__((aligned(1024))) char lds[4 * TILE];  // K0 K1 V0 V1
 
@@ -129,6 +165,9 @@ __global__ __launch_bounds__(NW * 64) void dq_bf16_kernel(BwdArgs a) {
   const float lse2 = qvalid ? a.lse[rowi] * kLog2e : INFINITY;
   const float dl = qvalid ? a.delta[rowi] : 0.f;
   const float slope = P.alibi ? P.alibi[h] : 0.f;
+  const bool by_interval = interval_mask(P);
+  int klo, khi;
+  key_interval(P, b, qw, &klo, &khi);
   const int qdoc = (P.q_doc && qvalid) ? P.q_doc[(size_t)b * P.Sq + qw] : 0;
 
   const char* kbase_ptr = static_cast<const char*>(a.k) + (size_t)(b * P.Hkv + hk) * P.Skv * RB;
@@ -160,12 +199,32 @@ __global__ __launch_bounds__(NW * 64) void dq_bf16_kernel(BwdArgs a) {
     }
   }
   const int n_it = walk.count();
-  auto issue = [&](int it, int buf) {
-    int kb;
-    bool msk;
-    walk.get(it, &kb, &msk);
+  auto issue = [&](int kb, int buf) {
     dma.issue(kbase_ptr, kb, P.Skv, lds + buf * TILE, w);
     dma.issue(vbase_ptr, kb, P.Skv, lds + (2 + buf) * TILE, w);
+  };
+
+  // dS^T from S^T (sacc) and dP^T (pacc), written into pacc
+  auto grad_scores = [&](f32x16* sacc, f32x16* pacc, int kbase, auto masked_c) {
+    constexpr bool kMasked = decltype(masked_c)::value;
+#pragma unroll
+    for (int j = 0; j < NSUB; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int key = kbase + 32 * j + acc_row(e, hh);
+        float dsdx = 1.f;
+        float t;
+        if constexpr (kMods) t = score_t<true>(P, sacc[j][e], slope, qw, key, &dsdx);
+        else t = sacc[j][e] * P.scale_log2;
+        if constexpr (kMasked) {
+          const bool ok = by_interval ? (key >= klo && key <= khi)
+                                      : (key < P.Skv && window_ok(P, qw, key) && qdoc == kv_doc_of(P, b, key));
+          t = ok ? t : -INFINITY;
+        }
+        const float pv = fast_exp2(t - lse2);
+        if constexpr (kMods) pacc[j][e] = pv * (pacc[j][e] - dl) * dsdx;
+        else pacc[j][e] = pv * (pacc[j][e] - dl);
+      }
   };
 
   f32x16 dqa[DT];
@@ -174,17 +233,22 @@ __global__ __launch_bounds__(NW * 64) void dq_bf16_kernel(BwdArgs a) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) dqa[i][e] = 0.f;
 
+  int kb_next = 0;
+  bool msk_next = false;
   if (n_it > 0) {
-    issue(0, 0);
+    walk.get(0, &kb_next, &msk_next);
+    issue(kb_next, 0);
     wait_vmem();
   }
   __syncthreads();
   for (int it = 0; it < n_it; ++it) {
     const int buf = it & 1;
-    if (it + 1 < n_it) issue(it + 1, buf ^ 1);
-    int kbase;
-    bool masked;
-    walk.get(it, &kbase, &masked);
+    const int kbase = kb_next;
+    bool masked = msk_next;
+    if (it + 1 < n_it) {
+      walk.get(it + 1, &kb_next, &msk_next);
+      issue(kb_next, buf ^ 1);
+    }
     if (kbase < P.Skv) {
       masked = masked || (kbase + BN > P.Skv);
       const char* kl = lds + buf * TILE;
@@ -194,39 +258,25 @@ __global__ __launch_bounds__(NW * 64) void dq_bf16_kernel(BwdArgs a) {
       for (int j = 0; j < NSUB; ++j)
 #pragma unroll
         for (int e = 0; e < 16; ++e) sacc[j][e] = pacc[j][e] = 0.f;
+      mma_rows2<D, NSUB>(rt, kl, vl, qf, df, sacc, pacc);
+      if (masked) grad_scores(sacc, pacc, kbase, std::true_type{});
+      else grad_scores(sacc, pacc, kbase, std::false_type{});
+      frag sf[NC];
 #pragma unroll
-      for (int s = 0; s < KSTEPS; ++s)
-#pragma unroll
-        for (int j = 0; j < NSUB; ++j) {
-          sacc[j] = E::mma(rt.a_frag(kl, j, s), qf[s], sacc[j]);
-          pacc[j] = E::mma(rt.a_frag(vl, j, s), df[s], pacc[j]);
-        }
-#pragma unroll
-      for (int j = 0; j < NSUB; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int key = kbase + 32 * j + acc_row(e, hh);
-          float dsdx = 1.f;
-          float t;
-          if constexpr (kMods) t = score_t<true>(P, sacc[j][e], slope, qw, key, &dsdx);
-          else t = sacc[j][e] * P.scale_log2;
-          if (masked && !(key < P.Skv && mask_ok(P, qw, key, qdoc, kv_doc_of(P, b, key)))) t = -INFINITY;
-          const float pv = fast_exp2(t - lse2);
-          if constexpr (kMods) pacc[j][e] = pv * (pacc[j][e] - dl) * dsdx;
-          else pacc[j][e] = pv * (pacc[j][e] - dl);
-        }
-      frag sf[BN / 16];
-#pragma unroll
-      for (int c = 0; c < BN / 16; ++c) {
+      for (int c = 0; c < NC; ++c) {
         float y[8];
 #pragma unroll
         for (int t = 0; t < 8; ++t) y[t] = pacc[c >> 1][8 * (c & 1) + t];
         sf[c] = E::pack(y);
       }
+      // dQ^T += K^T dS^T, K^T fragments fetched one step ahead
+      frag kt[2];
+      kt[0] = rt.t_frag(kl, 0, 0);
 #pragma unroll
-      for (int i = 0; i < DT; ++i)
-#pragma unroll
-        for (int c = 0; c < BN / 16; ++c) dqa[i] = E::mma(rt.t_frag(kl, i, c), sf[c], dqa[i]);
+      for (int x = 0; x < DT * NC; ++x) {
+        if (x + 1 < DT * NC) kt[(x + 1) & 1] = rt.t_frag(kl, (x + 1) / NC, (x + 1) % NC);
+        dqa[x / NC] = E::mma(kt[x & 1], sf[x % NC], dqa[x / NC]);
+      }
     }
     wait_vmem();
     __syncthreads();
@@ -256,6 +306,7 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   constexpr int KSTEPS = D / 16;
   constexpr int NQS = BQ / 32;
   constexpr int DT = D / 32;
+  constexpr int NC = BQ / 16;
   constexpr int TILE = BQ * RB;
   constexpr int STAT = 1024;  // LSE / Delta landing zone per buffer (BQ floats used)
   static_assert(BQ * 4 <= STAT, "stat tile");
@@ -283,6 +334,9 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
       vf[s] = buf_load16(rv, kw * RB + (2 * s + hh) * 16);
     }
   }
+  const bool by_interval = interval_mask(P);
+  int qlo, qhi;
+  query_interval(P, b, kw, &qlo, &qhi);
   const int kdoc = (P.q_doc && kvalid) ? P.kv_doc[(size_t)b * P.Skv + kw] : 0;
 
   RowTile<D> rt;
@@ -302,10 +356,7 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   walk.ntiles_dense = (P.Sq + BQ - 1) / BQ;
   const int n_it = walk.count();
 
-  auto issue = [&](int it, int buf) {
-    int hq, qb;
-    bool msk;
-    walk.get(it, &hq, &qb, &msk);
+  auto issue = [&](int hq, int qb, int buf) {
     const size_t hoff = (size_t)(b * P.Hq + hq) * P.Sq;
     dma.issue(static_cast<const char*>(a.q) + hoff * RB, qb, P.Sq, lds + buf * TILE, w);
     dma.issue(static_cast<const char*>(a.dout) + hoff * RB, qb, P.Sq, lds + (2 + buf) * TILE, w);
@@ -319,26 +370,64 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
     }
   };
 
+  // P (sacc) and dS (pacc) from S and dP; rows = queries, column = this lane's key
+  auto grad_scores = [&](f32x16* sacc, f32x16* pacc, int hq, int qbase, const float* lsel, const float* dltl,
+                         auto masked_c) {
+    constexpr bool kMasked = decltype(masked_c)::value;
+    const float slope = P.alibi ? P.alibi[hq] : 0.f;
+#pragma unroll
+    for (int j = 0; j < NQS; ++j)
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const int r0 = 32 * j + acc_row(4 * e4, hh);
+        const f32x4 ls = *reinterpret_cast<const f32x4*>(lsel + r0);
+        const f32x4 dt4 = *reinterpret_cast<const f32x4*>(dltl + r0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int e = 4 * e4 + i;
+          const int qi = qbase + r0 + i;
+          float dsdx = 1.f;
+          float t;
+          if constexpr (kMods) t = score_t<true>(P, sacc[j][e], slope, qi, kw, &dsdx);
+          else t = sacc[j][e] * P.scale_log2;
+          if constexpr (kMasked) {
+            const bool ok = by_interval
+                                ? (qi >= qlo && qi <= qhi)
+                                : (kvalid && qi < P.Sq && window_ok(P, qi, kw) && q_doc_of(P, b, qi) == kdoc);
+            t = ok ? t : -INFINITY;
+          }
+          const float pv = fast_exp2(t - ls[i] * kLog2e);
+          sacc[j][e] = pv;
+          if constexpr (kMods) pacc[j][e] = pv * (pacc[j][e] - dt4[i]) * dsdx;
+          else pacc[j][e] = pv * (pacc[j][e] - dt4[i]);
+        }
+      }
+  };
+
   f32x16 dka[DT], dva[DT];
 #pragma unroll
   for (int i = 0; i < DT; ++i)
 #pragma unroll
     for (int e = 0; e < 16; ++e) dka[i][e] = dva[i][e] = 0.f;
 
+  int hq_next = 0, qb_next = 0;
+  bool msk_next = false;
   if (n_it > 0) {
-    issue(0, 0);
+    walk.get(0, &hq_next, &qb_next, &msk_next);
+    issue(hq_next, qb_next, 0);
     wait_vmem();
   }
   __syncthreads();
   for (int it = 0; it < n_it; ++it) {
     const int buf = it & 1;
-    if (it + 1 < n_it) issue(it + 1, buf ^ 1);
-    int hq, qbase;
-    bool masked;
-    walk.get(it, &hq, &qbase, &masked);
+    const int hq = hq_next, qbase = qb_next;
+    bool masked = msk_next;
+    if (it + 1 < n_it) {
+      walk.get(it + 1, &hq_next, &qb_next, &msk_next);
+      issue(hq_next, qb_next, buf ^ 1);
+    }
     if (qbase < P.Sq) {
       masked = masked || (k0 + BKV > P.Skv) || (qbase + BQ > P.Sq);
-      const float slope = P.alibi ? P.alibi[hq] : 0.f;
       const char* ql = lds + buf * TILE;
       const char* dl_ = lds + (2 + buf) * TILE;
       const float* lsel = reinterpret_cast<const float*>(lds + 4 * TILE + buf * STAT);
@@ -349,38 +438,13 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
       for (int j = 0; j < NQS; ++j)
 #pragma unroll
         for (int e = 0; e < 16; ++e) sacc[j][e] = pacc[j][e] = 0.f;
+      mma_rows2<D, NQS>(rt, ql, dl_, kf, vf, sacc, pacc);
+      if (masked) grad_scores(sacc, pacc, hq, qbase, lsel, dltl, std::true_type{});
+      else grad_scores(sacc, pacc, hq, qbase, lsel, dltl, std::false_type{});
+
+      frag pf[NC], sf[NC];
 #pragma unroll
-      for (int s = 0; s < KSTEPS; ++s)
-#pragma unroll
-        for (int j = 0; j < NQS; ++j) {
-          sacc[j] = E::mma(rt.a_frag(ql, j, s), kf[s], sacc[j]);
-          pacc[j] = E::mma(rt.a_frag(dl_, j, s), vf[s], pacc[j]);
-        }
-#pragma unroll
-      for (int j = 0; j < NQS; ++j)
-#pragma unroll
-        for (int e4 = 0; e4 < 4; ++e4) {
-          const int r0 = 32 * j + acc_row(4 * e4, hh);
-          const f32x4 ls = *reinterpret_cast<const f32x4*>(lsel + r0);
-          const f32x4 dt4 = *reinterpret_cast<const f32x4*>(dltl + r0);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int e = 4 * e4 + i;
-            const int qi = qbase + r0 + i;
-            float dsdx = 1.f;
-            float t;
-            if constexpr (kMods) t = score_t<true>(P, sacc[j][e], slope, qi, kw, &dsdx);
-            else t = sacc[j][e] * P.scale_log2;
-            if (masked && !(kvalid && qi < P.Sq && mask_ok(P, qi, kw, q_doc_of(P, b, qi), kdoc))) t = -INFINITY;
-            const float pv = fast_exp2(t - ls[i] * kLog2e);
-            sacc[j][e] = pv;
-            if constexpr (kMods) pacc[j][e] = pv * (pacc[j][e] - dt4[i]) * dsdx;
-            else pacc[j][e] = pv * (pacc[j][e] - dt4[i]);
-          }
-        }
-      frag pf[BQ / 16], sf[BQ / 16];
-#pragma unroll
-      for (int c = 0; c < BQ / 16; ++c) {
+      for (int c = 0; c < NC; ++c) {
         float x[8], y[8];
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
@@ -390,13 +454,19 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
         pf[c] = E::pack(x);
         sf[c] = E::pack(y);
       }
+      // dV^T += dO^T P, dK^T += Q^T dS; transposed fragments fetched one step ahead
+      frag ft[2][2];
+      ft[0][0] = rt.t_frag(dl_, 0, 0);
+      ft[0][1] = rt.t_frag(ql, 0, 0);
 #pragma unroll
-      for (int i = 0; i < DT; ++i)
-#pragma unroll
-        for (int c = 0; c < BQ / 16; ++c) {
-          dva[i] = E::mma(rt.t_frag(dl_, i, c), pf[c], dva[i]);
-          dka[i] = E::mma(rt.t_frag(ql, i, c), sf[c], dka[i]);
+      for (int x = 0; x < DT * NC; ++x) {
+        if (x + 1 < DT * NC) {
+          ft[(x + 1) & 1][0] = rt.t_frag(dl_, (x + 1) / NC, (x + 1) % NC);
+          ft[(x + 1) & 1][1] = rt.t_frag(ql, (x + 1) / NC, (x + 1) % NC);
         }
+        dva[x / NC] = E::mma(ft[x & 1][0], pf[x % NC], dva[x / NC]);
+        dka[x / NC] = E::mma(ft[x & 1][1], sf[x % NC], dka[x / NC]);
+      }
     }
     wait_vmem();
     __syncthreads();
