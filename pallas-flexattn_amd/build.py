@@ -16,6 +16,9 @@ FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-shared", "-fPIC",
     # keep packed-fp32 VALU instructions out of the generated code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs where they fit: fewer AGPR<->VGPR copies in
+    # the backward kernels (about 3% faster there, forward unchanged)
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-I" + os.path.join(REPO, "include"),
 ]
 

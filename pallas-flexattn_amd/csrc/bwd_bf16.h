@@ -18,8 +18,9 @@
 //   dkdv_bf16_kernel (batch, kv head, 32*NW keys): K, V rows in VGPRs;
 //                    S = Q K^T, dP = dO V^T, dV^T += dO^T P, dK^T += Q^T dS
 //                    over the q-side tables of every q head of the GQA group.
-// Partial tiles apply the element mask (an interval per lane for windows and
-// contiguous documents); full tiles skip it.
+// Partial tiles apply the element mask, an interval per lane (windows and
+// contiguous documents; other document layouts use the generic kernels);
+// full tiles skip it.
 #pragma once
 #include <type_traits>
 
@@ -95,34 +96,30 @@ struct TileDma {
   }
 };
 
-// acc[j] += A(tileA rows, j) * bA[s]  and  acc2[j] += A(tileB rows, j) * bB[s]
+// acc += A(tileA rows 32j..) * bA[s]  and  acc2 += A(tileB rows 32j..) * bB[s]
 // over all k steps, operands fetched one step ahead.
-template <int D, int NJ>
-__device__ __forceinline__ void mma_rows2(const RowTile<D>& rt, const char* ta, const char* tb,
-                                          const u32x4* ba, const u32x4* bb, f32x16* acc, f32x16* acc2) {
+template <int D>
+__device__ __forceinline__ void mma_rows2(const RowTile<D>& rt, const char* ta, const char* tb, int j,
+                                          const u32x4* ba, const u32x4* bb, f32x16& acc, f32x16& acc2) {
   using E = Elt<uint16_t>;
   constexpr int KS = D / 16;
-  u32x4 fa[2][NJ], fb[2][NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    fa[0][j] = rt.a_frag(ta, j, 0);
-    fb[0][j] = rt.a_frag(tb, j, 0);
-  }
+  u32x4 fa[2], fb[2];
+  fa[0] = rt.a_frag(ta, j, 0);
+  fb[0] = rt.a_frag(tb, j, 0);
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
     if (s + 1 < KS) {
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        fa[(s + 1) & 1][j] = rt.a_frag(ta, j, s + 1);
-        fb[(s + 1) & 1][j] = rt.a_frag(tb, j, s + 1);
-      }
+      fa[(s + 1) & 1] = rt.a_frag(ta, j, s + 1);
+      fb[(s + 1) & 1] = rt.a_frag(tb, j, s + 1);
     }
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      acc[j] = E::mma(fa[s & 1][j], ba[s], acc[j]);
-      acc2[j] = E::mma(fb[s & 1][j], bb[s], acc2[j]);
-    }
+    acc = E::mma(fa[s & 1], ba[s], acc);
+    acc2 = E::mma(fb[s & 1], bb[s], acc2);
   }
+}
+
+__device__ __forceinline__ void zero(f32x16& x) {
+#pragma unroll
+  for (int e = 0; e < 16; ++e) x[e] = 0.f;
 }
 
 // ------------------------------------------------------------------- dQ ----
@@ -165,10 +162,8 @@ __global__ __launch_bounds__(NW * 64) void dq_bf16_kernel(BwdArgs a) {
   const float lse2 = qvalid ? a.lse[rowi] * kLog2e : INFINITY;
   const float dl = qvalid ? a.delta[rowi] : 0.f;
   const float slope = P.alibi ? P.alibi[h] : 0.f;
-  const bool by_interval = interval_mask(P);
-  int klo, khi;
+  int klo, khi;  // keys visible to this lane's query (masks are intervals here)
   key_interval(P, b, qw, &klo, &khi);
-  const int qdoc = (P.q_doc && qvalid) ? P.q_doc[(size_t)b * P.Sq + qw] : 0;
 
   const char* kbase_ptr = static_cast<const char*>(a.k) + (size_t)(b * P.Hkv + hk) * P.Skv * RB;
   const char* vbase_ptr = static_cast<const char*>(a.v) + (size_t)(b * P.Hkv + hk) * P.Skv * RB;
@@ -204,34 +199,59 @@ __global__ __launch_bounds__(NW * 64) void dq_bf16_kernel(BwdArgs a) {
     dma.issue(vbase_ptr, kb, P.Skv, lds + (2 + buf) * TILE, w);
   };
 
-  // dS^T from S^T (sacc) and dP^T (pacc), written into pacc
-  auto grad_scores = [&](f32x16* sacc, f32x16* pacc, int kbase, auto masked_c) {
-    constexpr bool kMasked = decltype(masked_c)::value;
-#pragma unroll
-    for (int j = 0; j < NSUB; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int key = kbase + 32 * j + acc_row(e, hh);
-        float dsdx = 1.f;
-        float t;
-        if constexpr (kMods) t = score_t<true>(P, sacc[j][e], slope, qw, key, &dsdx);
-        else t = sacc[j][e] * P.scale_log2;
-        if constexpr (kMasked) {
-          const bool ok = by_interval ? (key >= klo && key <= khi)
-                                      : (key < P.Skv && window_ok(P, qw, key) && qdoc == kv_doc_of(P, b, key));
-          t = ok ? t : -INFINITY;
-        }
-        const float pv = fast_exp2(t - lse2);
-        if constexpr (kMods) pacc[j][e] = pv * (pacc[j][e] - dl) * dsdx;
-        else pacc[j][e] = pv * (pacc[j][e] - dl);
-      }
-  };
-
   f32x16 dqa[DT];
 #pragma unroll
-  for (int i = 0; i < DT; ++i)
+  for (int i = 0; i < DT; ++i) zero(dqa[i]);
+
+  // One kv tile: per 32-key sub-tile S^T, dP^T -> dS^T (packed), then dQ^T += K^T dS^T.
+  auto tile = [&](int kbase, const char* kl, const char* vl, auto masked_c) {
+    constexpr bool kMasked = decltype(masked_c)::value;
+    frag sf[NC];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) dqa[i][e] = 0.f;
+    for (int j = 0; j < NSUB; ++j) {
+      f32x16 sacc, pacc;
+      zero(sacc);
+      zero(pacc);
+      mma_rows2<D>(rt, kl, vl, j, qf, df, sacc, pacc);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        float dsdx = 1.f;
+        float pv;
+        if constexpr (kMods) {
+          float t = score_t<true>(P, sacc[e], slope, qw, kbase + 32 * j + acc_row(e, hh), &dsdx);
+          if constexpr (kMasked) {
+            const int key = kbase + 32 * j + acc_row(e, hh);
+            t = (key >= klo && key <= khi) ? t : -INFINITY;
+          }
+          pv = fast_exp2(t - lse2);
+        } else {
+          float x = sacc[e];
+          if constexpr (kMasked) {
+            const int key = kbase + 32 * j + acc_row(e, hh);
+            x = (key >= klo && key <= khi) ? x : -INFINITY;
+          }
+          pv = fast_exp2(fmaf(x, P.scale_log2, -lse2));
+        }
+        if constexpr (kMods) pacc[e] = pv * (pacc[e] - dl) * dsdx;
+        else pacc[e] = pv * (pacc[e] - dl);
+      }
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        float y[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) y[t] = pacc[8 * half + t];
+        sf[2 * j + half] = E::pack(y);
+      }
+    }
+    // dQ^T += K^T dS^T, K^T fragments fetched one step ahead
+    frag kt[2];
+    kt[0] = rt.t_frag(kl, 0, 0);
+#pragma unroll
+    for (int x = 0; x < DT * NC; ++x) {
+      if (x + 1 < DT * NC) kt[(x + 1) & 1] = rt.t_frag(kl, (x + 1) / NC, (x + 1) % NC);
+      dqa[x / NC] = E::mma(kt[x & 1], sf[x % NC], dqa[x / NC]);
+    }
+  };
 
   int kb_next = 0;
   bool msk_next = false;
@@ -253,30 +273,8 @@ __global__ __launch_bounds__(NW * 64) void dq_bf16_kernel(BwdArgs a) {
       masked = masked || (kbase + BN > P.Skv);
       const char* kl = lds + buf * TILE;
       const char* vl = lds + (2 + buf) * TILE;
-      f32x16 sacc[NSUB], pacc[NSUB];
-#pragma unroll
-      for (int j = 0; j < NSUB; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) sacc[j][e] = pacc[j][e] = 0.f;
-      mma_rows2<D, NSUB>(rt, kl, vl, qf, df, sacc, pacc);
-      if (masked) grad_scores(sacc, pacc, kbase, std::true_type{});
-      else grad_scores(sacc, pacc, kbase, std::false_type{});
-      frag sf[NC];
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        float y[8];
-#pragma unroll
-        for (int t = 0; t < 8; ++t) y[t] = pacc[c >> 1][8 * (c & 1) + t];
-        sf[c] = E::pack(y);
-      }
-      // dQ^T += K^T dS^T, K^T fragments fetched one step ahead
-      frag kt[2];
-      kt[0] = rt.t_frag(kl, 0, 0);
-#pragma unroll
-      for (int x = 0; x < DT * NC; ++x) {
-        if (x + 1 < DT * NC) kt[(x + 1) & 1] = rt.t_frag(kl, (x + 1) / NC, (x + 1) % NC);
-        dqa[x / NC] = E::mma(kt[x & 1], sf[x % NC], dqa[x / NC]);
-      }
+      if (masked) tile(kbase, kl, vl, std::true_type{});
+      else tile(kbase, kl, vl, std::false_type{});
     }
     wait_vmem();
     __syncthreads();
@@ -334,10 +332,8 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
       vf[s] = buf_load16(rv, kw * RB + (2 * s + hh) * 16);
     }
   }
-  const bool by_interval = interval_mask(P);
-  int qlo, qhi;
+  int qlo, qhi;  // queries that see this lane's key (masks are intervals here)
   query_interval(P, b, kw, &qlo, &qhi);
-  const int kdoc = (P.q_doc && kvalid) ? P.kv_doc[(size_t)b * P.Skv + kw] : 0;
 
   RowTile<D> rt;
   rt.init(lane);
@@ -370,13 +366,26 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
     }
   };
 
-  // P (sacc) and dS (pacc) from S and dP; rows = queries, column = this lane's key
-  auto grad_scores = [&](f32x16* sacc, f32x16* pacc, int hq, int qbase, const float* lsel, const float* dltl,
-                         auto masked_c) {
+  f32x16 dka[DT], dva[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i) {
+    zero(dka[i]);
+    zero(dva[i]);
+  }
+
+  // One q tile: per 32-query sub-tile S, dP -> P, dS (packed, rows = queries,
+  // column = this lane's key), then dV^T += dO^T P and dK^T += Q^T dS.
+  auto tile = [&](int hq, int qbase, const char* ql, const char* dl_, const float* lsel, const float* dltl,
+                  auto masked_c) {
     constexpr bool kMasked = decltype(masked_c)::value;
     const float slope = P.alibi ? P.alibi[hq] : 0.f;
+    frag pf[NC], sf[NC];
 #pragma unroll
-    for (int j = 0; j < NQS; ++j)
+    for (int j = 0; j < NQS; ++j) {
+      f32x16 sacc, pacc;
+      zero(sacc);
+      zero(pacc);
+      mma_rows2<D>(rt, ql, dl_, j, kf, vf, sacc, pacc);
 #pragma unroll
       for (int e4 = 0; e4 < 4; ++e4) {
         const int r0 = 32 * j + acc_row(4 * e4, hh);
@@ -387,28 +396,47 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
           const int e = 4 * e4 + i;
           const int qi = qbase + r0 + i;
           float dsdx = 1.f;
-          float t;
-          if constexpr (kMods) t = score_t<true>(P, sacc[j][e], slope, qi, kw, &dsdx);
-          else t = sacc[j][e] * P.scale_log2;
-          if constexpr (kMasked) {
-            const bool ok = by_interval
-                                ? (qi >= qlo && qi <= qhi)
-                                : (kvalid && qi < P.Sq && window_ok(P, qi, kw) && q_doc_of(P, b, qi) == kdoc);
-            t = ok ? t : -INFINITY;
+          float pv;
+          if constexpr (kMods) {
+            float t = score_t<true>(P, sacc[e], slope, qi, kw, &dsdx);
+            if constexpr (kMasked) t = (qi >= qlo && qi <= qhi) ? t : -INFINITY;
+            pv = fast_exp2(t - ls[i] * kLog2e);
+          } else {
+            float x = sacc[e];
+            if constexpr (kMasked) x = (qi >= qlo && qi <= qhi) ? x : -INFINITY;
+            pv = fast_exp2(fmaf(x, P.scale_log2, -ls[i] * kLog2e));
           }
-          const float pv = fast_exp2(t - ls[i] * kLog2e);
-          sacc[j][e] = pv;
-          if constexpr (kMods) pacc[j][e] = pv * (pacc[j][e] - dt4[i]) * dsdx;
-          else pacc[j][e] = pv * (pacc[j][e] - dt4[i]);
+          sacc[e] = pv;
+          if constexpr (kMods) pacc[e] = pv * (pacc[e] - dt4[i]) * dsdx;
+          else pacc[e] = pv * (pacc[e] - dt4[i]);
         }
       }
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        float x[8], y[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          x[t] = sacc[8 * half + t];
+          y[t] = pacc[8 * half + t];
+        }
+        pf[2 * j + half] = E::pack(x);
+        sf[2 * j + half] = E::pack(y);
+      }
+    }
+    // dV^T += dO^T P, dK^T += Q^T dS; transposed fragments fetched one step ahead
+    frag ft[2][2];
+    ft[0][0] = rt.t_frag(dl_, 0, 0);
+    ft[0][1] = rt.t_frag(ql, 0, 0);
+#pragma unroll
+    for (int x = 0; x < DT * NC; ++x) {
+      if (x + 1 < DT * NC) {
+        ft[(x + 1) & 1][0] = rt.t_frag(dl_, (x + 1) / NC, (x + 1) % NC);
+        ft[(x + 1) & 1][1] = rt.t_frag(ql, (x + 1) / NC, (x + 1) % NC);
+      }
+      dva[x / NC] = E::mma(ft[x & 1][0], pf[x % NC], dva[x / NC]);
+      dka[x / NC] = E::mma(ft[x & 1][1], sf[x % NC], dka[x / NC]);
+    }
   };
-
-  f32x16 dka[DT], dva[DT];
-#pragma unroll
-  for (int i = 0; i < DT; ++i)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) dka[i][e] = dva[i][e] = 0.f;
 
   int hq_next = 0, qb_next = 0;
   bool msk_next = false;
@@ -432,41 +460,8 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
       const char* dl_ = lds + (2 + buf) * TILE;
       const float* lsel = reinterpret_cast<const float*>(lds + 4 * TILE + buf * STAT);
       const float* dltl = reinterpret_cast<const float*>(lds + 4 * TILE + (2 + buf) * STAT);
-
-      f32x16 sacc[NQS], pacc[NQS];
-#pragma unroll
-      for (int j = 0; j < NQS; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) sacc[j][e] = pacc[j][e] = 0.f;
-      mma_rows2<D, NQS>(rt, ql, dl_, kf, vf, sacc, pacc);
-      if (masked) grad_scores(sacc, pacc, hq, qbase, lsel, dltl, std::true_type{});
-      else grad_scores(sacc, pacc, hq, qbase, lsel, dltl, std::false_type{});
-
-      frag pf[NC], sf[NC];
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        float x[8], y[8];
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          x[t] = sacc[c >> 1][8 * (c & 1) + t];
-          y[t] = pacc[c >> 1][8 * (c & 1) + t];
-        }
-        pf[c] = E::pack(x);
-        sf[c] = E::pack(y);
-      }
-      // dV^T += dO^T P, dK^T += Q^T dS; transposed fragments fetched one step ahead
-      frag ft[2][2];
-      ft[0][0] = rt.t_frag(dl_, 0, 0);
-      ft[0][1] = rt.t_frag(ql, 0, 0);
-#pragma unroll
-      for (int x = 0; x < DT * NC; ++x) {
-        if (x + 1 < DT * NC) {
-          ft[(x + 1) & 1][0] = rt.t_frag(dl_, (x + 1) / NC, (x + 1) % NC);
-          ft[(x + 1) & 1][1] = rt.t_frag(ql, (x + 1) / NC, (x + 1) % NC);
-        }
-        dva[x / NC] = E::mma(ft[x & 1][0], pf[x % NC], dva[x / NC]);
-        dka[x / NC] = E::mma(ft[x & 1][1], sf[x % NC], dka[x / NC]);
-      }
+      if (masked) tile(hq, qbase, ql, dl_, lsel, dltl, std::true_type{});
+      else tile(hq, qbase, ql, dl_, lsel, dltl, std::false_type{});
     }
     wait_vmem();
     __syncthreads();

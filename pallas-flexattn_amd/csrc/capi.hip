@@ -101,16 +101,21 @@ int build_problem(const fa_params* p, const Tiles& t, Problem* pr) {
 
 int launch_status() { return hipGetLastError() == hipSuccess ? FA_OK : FA_ERR_LAUNCH; }
 
+// The bf16 LDS-DMA kernels evaluate masks as per-lane intervals (windows and
+// contiguous documents); arbitrary document labels go to the generic kernels.
+bool interval_masks(const Problem& p) { return p.q_doc == nullptr || p.doc_start != nullptr; }
+
 // ------------------------------------------------------------- forward ----
 template <typename T, int D, int BN, int NW, bool M>
 int run_fwd(const FwdArgs& a, hipStream_t s) {
   const int grid = a.p.B * a.p.Hq * cdiv(a.p.Sq, 32 * NW);
   if constexpr (sizeof(T) == 2) {
-    // bf16: LDS-DMA + transposing-read kernel
-    hipLaunchKernelGGL((fa::fwd_bf16_kernel<D, BN, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
-  } else {
-    hipLaunchKernelGGL((fa::fwd_kernel<T, D, BN, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
+    if (interval_masks(a.p)) {  // bf16: LDS-DMA + transposing-read kernel
+      hipLaunchKernelGGL((fa::fwd_bf16_kernel<D, BN, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
+      return launch_status();
+    }
   }
+  hipLaunchKernelGGL((fa::fwd_kernel<T, D, BN, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
   return launch_status();
 }
 
@@ -135,10 +140,12 @@ template <typename T, int D, int BN, int NW, bool M>
 int run_dq(const BwdArgs& a, hipStream_t s) {
   const int grid = a.p.B * a.p.Hq * cdiv(a.p.Sq, 32 * NW);
   if constexpr (sizeof(T) == 2) {
-    hipLaunchKernelGGL((fa::dq_bf16_kernel<D, BN, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
-  } else {
-    hipLaunchKernelGGL((fa::dq_kernel<T, D, BN, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
+    if (interval_masks(a.p)) {
+      hipLaunchKernelGGL((fa::dq_bf16_kernel<D, BN, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
+      return launch_status();
+    }
   }
+  hipLaunchKernelGGL((fa::dq_kernel<T, D, BN, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
   return launch_status();
 }
 
@@ -146,10 +153,12 @@ template <typename T, int D, int BQ, int NW, bool M>
 int run_dkdv(const BwdArgs& a, hipStream_t s) {
   const int grid = a.p.B * a.p.Hkv * cdiv(a.p.Skv, 32 * NW);
   if constexpr (sizeof(T) == 2) {
-    hipLaunchKernelGGL((fa::dkdv_bf16_kernel<D, BQ, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
-  } else {
-    hipLaunchKernelGGL((fa::dkdv_kernel<T, D, BQ, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
+    if (interval_masks(a.p)) {
+      hipLaunchKernelGGL((fa::dkdv_bf16_kernel<D, BQ, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
+      return launch_status();
+    }
   }
+  hipLaunchKernelGGL((fa::dkdv_kernel<T, D, BQ, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
   return launch_status();
 }
 

@@ -10,11 +10,12 @@
 //   * S^T = K Q^T   (A = K rows from LDS in perm23 order, fetched one k-step
 //     ahead of the MFMAs; B = Q from VGPRs);
 //   * online softmax with one query per lane: row max / sum are per-lane
-//     scalars plus a v_permlane32_swap between lane halves; O is rescaled only
-//     when some row maximum grew (multiplying by exp2(0) = 1 is skipped, so
-//     results are unchanged); fully-live tiles skip the element mask, partial
-//     tiles test key in [lo, hi] (window and contiguous documents are
-//     intervals per query) or compare document ids;
+//     scalars plus a v_permlane32_swap between lane halves; the reference
+//     maximum may trail the running one by up to 2^8 in P, so O is rescaled
+//     only when some row maximum outgrows that; the scale is folded into the
+//     exponent's FMA; fully-live tiles skip the element mask, partial tiles
+//     keep keys in [lo, hi] (window and contiguous documents are intervals
+//     per query);
 //   * O^T += V^T P^T (A = V^T fetched from the row-major V tile with
 //     ds_read_b64_tr_b16, B = P^T straight from the S^T accumulators).
 // LDS layouts (row = key, 16-byte chunks): K chunk c of row r sits in slot
@@ -71,10 +72,10 @@ void fwd_bf16_kernel(FwdArgs a) {
     for (int s = 0; s < KSTEPS; ++s) qf[s] = buf_load16(rq, qw * RB + (2 * s + hh) * 16);
   }
   const float slope = P.alibi ? P.alibi[h] : 0.f;
-  const bool by_interval = interval_mask(P);
+  // every mask term is an interval of keys per query (the host routes
+  // arbitrary document labels to the generic kernel)
   int klo, khi;
   key_interval(P, b, qw, &klo, &khi);
-  const int qdoc = (P.q_doc && qvalid) ? P.q_doc[(size_t)b * P.Sq + qw] : 0;
 
   // loop-invariant LDS / global offsets
   int dma_off_k[IPW], dma_off_v[IPW];
@@ -142,30 +143,26 @@ void fwd_bf16_kernel(FwdArgs a) {
   for (int i = 0; i < DT; ++i)
 #pragma unroll
     for (int e = 0; e < 16; ++e) oacc[i][e] = 0.f;
-  float m = -INFINITY, l = 0.f;  // running max in log2 units, per-lane partial sum
+  // Reference maximum m (log2 units, per row) and partial sum l.  m may trail
+  // the running maximum by up to kSlack: P = exp2(t - m) then stays below
+  // 2^kSlack, and O, l are rescaled only when a row maximum outgrows it (the
+  // normalisation O / l does not depend on which reference is used).
+  constexpr float kSlack = 8.0f;
+  float m = -INFINITY, l = 0.f;
 
-  // softmax of one tile held in sacc (log2-domain logits written back as P)
-  auto softmax = [&](f32x16* sacc, int kbase, auto masked_c) {
-    constexpr bool kMasked = decltype(masked_c)::value;
+  // Online softmax of one tile held in sacc.  Without score mods sacc keeps
+  // raw q.k: the max is taken on it (scale > 0) and the scale is folded into
+  // the exponent's FMA.  With mods sacc holds log2-domain logits.
+  auto softmax = [&](f32x16* sacc) {
     float mx = -INFINITY;
 #pragma unroll
     for (int j = 0; j < NSUB; ++j)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int key = kbase + 32 * j + acc_row(e, hh);
-        float t;
-        if constexpr (kMods) t = score_t<true>(P, sacc[j][e], slope, qw, key, nullptr);
-        else t = sacc[j][e] * P.scale_log2;
-        if constexpr (kMasked) {
-          const bool ok = by_interval ? (key >= klo && key <= khi)
-                                      : (key < P.Skv && window_ok(P, qw, key) && qdoc == kv_doc_of(P, b, key));
-          t = ok ? t : -INFINITY;
-        }
-        sacc[j][e] = t;
-        mx = fmaxf(mx, t);
-      }
-    const float mnew = fmaxf(m, pair_max(mx));
-    if (__any(mnew > m)) {
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sacc[j][e]);
+    float mt = pair_max(mx);
+    if constexpr (!kMods) mt *= P.scale_log2;
+    const float mnew = fmaxf(m, mt);
+    if (__any(mnew > m + kSlack)) {
       const float alpha = fast_exp2(m - (mnew == -INFINITY ? 0.f : mnew));
       l *= alpha;
 #pragma unroll
@@ -180,7 +177,9 @@ void fwd_bf16_kernel(FwdArgs a) {
     for (int j = 0; j < NSUB; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const float pv = fast_exp2(sacc[j][e] - muse);
+        float pv;
+        if constexpr (kMods) pv = fast_exp2(sacc[j][e] - muse);
+        else pv = fast_exp2(fmaf(sacc[j][e], P.scale_log2, -muse));
         sacc[j][e] = pv;
         rs += pv;
       }
@@ -227,8 +226,23 @@ void fwd_bf16_kernel(FwdArgs a) {
         for (int j = 0; j < NSUB; ++j) sacc[j] = E::mma(ka[s & 1][j], qf[s], sacc[j]);
       }
 
-      if (masked) softmax(sacc, kbase, std::true_type{});
-      else softmax(sacc, kbase, std::false_type{});
+      if constexpr (kMods) {
+#pragma unroll
+        for (int j = 0; j < NSUB; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            sacc[j][e] = score_t<true>(P, sacc[j][e], slope, qw, kbase + 32 * j + acc_row(e, hh), nullptr);
+      }
+      if (masked) {  // partial tile: keys outside [klo, khi] are dropped
+#pragma unroll
+        for (int j = 0; j < NSUB; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int key = kbase + 32 * j + acc_row(e, hh);
+            sacc[j][e] = (key >= klo && key <= khi) ? sacc[j][e] : -INFINITY;
+          }
+      }
+      softmax(sacc);
 
       frag pf[BN / 16];
 #pragma unroll
