@@ -199,40 +199,47 @@ __global__ __launch_bounds__(NW * 64) void dq_bf16_kernel(BwdArgs a) {
     dma.issue(vbase_ptr, kb, P.Skv, lds + (2 + buf) * TILE, w);
   };
 
-  f32x16 dqa[DT];
+  f32x16 dqa[DT];  // AGPRs, accumulated in place
 #pragma unroll
-  for (int i = 0; i < DT; ++i) zero(dqa[i]);
+  for (int i = 0; i < DT; ++i) {
+    zero(dqa[i]);
+    mfma_drain(dqa[i]);
+  }
 
-  // One kv tile: per 32-key sub-tile S^T, dP^T -> dS^T (packed), then dQ^T += K^T dS^T.
-  auto tile = [&](int kbase, const char* kl, const char* vl, auto masked_c) {
-    constexpr bool kMasked = decltype(masked_c)::value;
-    frag sf[NC];
+  // One kv tile: per 32-key sub-tile S^T, dP^T -> dS^T (packed), then that
+  // sub-tile's share of dQ^T += K^T dS^T (K^T fragments one step ahead), so
+  // the next sub-tile's MFMAs can overlap this one's exponentials.
+  // A single code path for full and partial tiles: only the in-place masking
+  // of S^T is conditional, so the loop-carried accumulators keep their
+  // registers.
+  auto tile = [&](int kbase, const char* kl, const char* vl, bool masked) {
+    frag sf[2];
 #pragma unroll
     for (int j = 0; j < NSUB; ++j) {
       f32x16 sacc, pacc;
       zero(sacc);
       zero(pacc);
       mma_rows2<D>(rt, kl, vl, j, qf, df, sacc, pacc);
+      float dsdx[16];
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        float dsdx = 1.f;
-        float pv;
-        if constexpr (kMods) {
-          float t = score_t<true>(P, sacc[e], slope, qw, kbase + 32 * j + acc_row(e, hh), &dsdx);
-          if constexpr (kMasked) {
-            const int key = kbase + 32 * j + acc_row(e, hh);
-            t = (key >= klo && key <= khi) ? t : -INFINITY;
-          }
-          pv = fast_exp2(t - lse2);
-        } else {
-          float x = sacc[e];
-          if constexpr (kMasked) {
-            const int key = kbase + 32 * j + acc_row(e, hh);
-            x = (key >= klo && key <= khi) ? x : -INFINITY;
-          }
-          pv = fast_exp2(fmaf(x, P.scale_log2, -lse2));
+        dsdx[e] = 1.f;
+        if constexpr (kMods)
+          sacc[e] = score_t<true>(P, sacc[e], slope, qw, kbase + 32 * j + acc_row(e, hh), &dsdx[e]);
+      }
+      if (masked) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int key = kbase + 32 * j + acc_row(e, hh);
+          sacc[e] = (key >= klo && key <= khi) ? sacc[e] : -INFINITY;
         }
-        if constexpr (kMods) pacc[e] = pv * (pacc[e] - dl) * dsdx;
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        float pv;
+        if constexpr (kMods) pv = fast_exp2(sacc[e] - lse2);
+        else pv = fast_exp2(fmaf(sacc[e], P.scale_log2, -lse2));
+        if constexpr (kMods) pacc[e] = pv * (pacc[e] - dl) * dsdx[e];
         else pacc[e] = pv * (pacc[e] - dl);
       }
 #pragma unroll
@@ -240,16 +247,16 @@ __global__ __launch_bounds__(NW * 64) void dq_bf16_kernel(BwdArgs a) {
         float y[8];
 #pragma unroll
         for (int t = 0; t < 8; ++t) y[t] = pacc[8 * half + t];
-        sf[2 * j + half] = E::pack(y);
+        sf[half] = E::pack(y);
       }
-    }
-    // dQ^T += K^T dS^T, K^T fragments fetched one step ahead
-    frag kt[2];
-    kt[0] = rt.t_frag(kl, 0, 0);
+      // x = (d tile, chunk half) of this sub-tile: chunk c = 2j + half
+      frag kt[2];
+      kt[0] = rt.t_frag(kl, 0, 2 * j);
 #pragma unroll
-    for (int x = 0; x < DT * NC; ++x) {
-      if (x + 1 < DT * NC) kt[(x + 1) & 1] = rt.t_frag(kl, (x + 1) / NC, (x + 1) % NC);
-      dqa[x / NC] = E::mma(kt[x & 1], sf[x % NC], dqa[x / NC]);
+      for (int x = 0; x < 2 * DT; ++x) {
+        if (x + 1 < 2 * DT) kt[(x + 1) & 1] = rt.t_frag(kl, (x + 1) >> 1, 2 * j + ((x + 1) & 1));
+        mfma_acc(dqa[x >> 1], kt[x & 1], sf[x & 1]);
+      }
     }
   };
 
@@ -271,15 +278,14 @@ __global__ __launch_bounds__(NW * 64) void dq_bf16_kernel(BwdArgs a) {
     }
     if (kbase < P.Skv) {
       masked = masked || (kbase + BN > P.Skv);
-      const char* kl = lds + buf * TILE;
-      const char* vl = lds + (2 + buf) * TILE;
-      if (masked) tile(kbase, kl, vl, std::true_type{});
-      else tile(kbase, kl, vl, std::false_type{});
+      tile(kbase, lds + buf * TILE, lds + (2 + buf) * TILE, masked);
     }
     wait_vmem();
     __syncthreads();
   }
 
+#pragma unroll
+  for (int i = 0; i < DT; ++i) mfma_drain(dqa[i]);
   if (qvalid) {
     uint16_t* dqp = static_cast<uint16_t*>(a.dq) + rowi * D;
 #pragma unroll
@@ -368,24 +374,43 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
 
   f32x16 dka[DT], dva[DT];
 #pragma unroll
-  for (int i = 0; i < DT; ++i) {
+  for (int i = 0; i < DT; ++i) {  // AGPRs, accumulated in place
     zero(dka[i]);
     zero(dva[i]);
+    mfma_drain(dka[i]);
+    mfma_drain(dva[i]);
   }
 
-  // One q tile: per 32-query sub-tile S, dP -> P, dS (packed, rows = queries,
-  // column = this lane's key), then dV^T += dO^T P and dK^T += Q^T dS.
+  // One q tile, one code path for full and partial tiles (only the in-place
+  // masking of S is conditional).  Per 32-query sub-tile: S, dP -> P, dS
+  // (packed, rows = queries, column = this lane's key), then that sub-tile's
+  // share of dV^T += dO^T P and dK^T += Q^T dS (transposed fragments one step
+  // ahead), so the next sub-tile's MFMAs can overlap this one's exponentials.
   auto tile = [&](int hq, int qbase, const char* ql, const char* dl_, const float* lsel, const float* dltl,
-                  auto masked_c) {
-    constexpr bool kMasked = decltype(masked_c)::value;
+                  bool masked) {
     const float slope = P.alibi ? P.alibi[hq] : 0.f;
-    frag pf[NC], sf[NC];
 #pragma unroll
     for (int j = 0; j < NQS; ++j) {
       f32x16 sacc, pacc;
       zero(sacc);
       zero(pacc);
       mma_rows2<D>(rt, ql, dl_, j, kf, vf, sacc, pacc);
+      float dsdx[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        dsdx[e] = 1.f;
+        if constexpr (kMods) {
+          const int qi = qbase + 32 * j + acc_row(e, hh);
+          sacc[e] = score_t<true>(P, sacc[e], slope, qi, kw, &dsdx[e]);
+        }
+      }
+      if (masked) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int qi = qbase + 32 * j + acc_row(e, hh);
+          sacc[e] = (qi >= qlo && qi <= qhi) ? sacc[e] : -INFINITY;
+        }
+      }
 #pragma unroll
       for (int e4 = 0; e4 < 4; ++e4) {
         const int r0 = 32 * j + acc_row(4 * e4, hh);
@@ -394,23 +419,15 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int e = 4 * e4 + i;
-          const int qi = qbase + r0 + i;
-          float dsdx = 1.f;
           float pv;
-          if constexpr (kMods) {
-            float t = score_t<true>(P, sacc[e], slope, qi, kw, &dsdx);
-            if constexpr (kMasked) t = (qi >= qlo && qi <= qhi) ? t : -INFINITY;
-            pv = fast_exp2(t - ls[i] * kLog2e);
-          } else {
-            float x = sacc[e];
-            if constexpr (kMasked) x = (qi >= qlo && qi <= qhi) ? x : -INFINITY;
-            pv = fast_exp2(fmaf(x, P.scale_log2, -ls[i] * kLog2e));
-          }
+          if constexpr (kMods) pv = fast_exp2(sacc[e] - ls[i] * kLog2e);
+          else pv = fast_exp2(fmaf(sacc[e], P.scale_log2, -ls[i] * kLog2e));
           sacc[e] = pv;
-          if constexpr (kMods) pacc[e] = pv * (pacc[e] - dt4[i]) * dsdx;
+          if constexpr (kMods) pacc[e] = pv * (pacc[e] - dt4[i]) * dsdx[e];
           else pacc[e] = pv * (pacc[e] - dt4[i]);
         }
       }
+      frag pf[2], sf[2];
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         float x[8], y[8];
@@ -419,22 +436,22 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
           x[t] = sacc[8 * half + t];
           y[t] = pacc[8 * half + t];
         }
-        pf[2 * j + half] = E::pack(x);
-        sf[2 * j + half] = E::pack(y);
+        pf[half] = E::pack(x);
+        sf[half] = E::pack(y);
       }
-    }
-    // dV^T += dO^T P, dK^T += Q^T dS; transposed fragments fetched one step ahead
-    frag ft[2][2];
-    ft[0][0] = rt.t_frag(dl_, 0, 0);
-    ft[0][1] = rt.t_frag(ql, 0, 0);
+      // x = (d tile, chunk half) of this sub-tile: chunk c = 2j + half
+      frag ft[2][2];
+      ft[0][0] = rt.t_frag(dl_, 0, 2 * j);
+      ft[0][1] = rt.t_frag(ql, 0, 2 * j);
 #pragma unroll
-    for (int x = 0; x < DT * NC; ++x) {
-      if (x + 1 < DT * NC) {
-        ft[(x + 1) & 1][0] = rt.t_frag(dl_, (x + 1) / NC, (x + 1) % NC);
-        ft[(x + 1) & 1][1] = rt.t_frag(ql, (x + 1) / NC, (x + 1) % NC);
+      for (int x = 0; x < 2 * DT; ++x) {
+        if (x + 1 < 2 * DT) {
+          ft[(x + 1) & 1][0] = rt.t_frag(dl_, (x + 1) >> 1, 2 * j + ((x + 1) & 1));
+          ft[(x + 1) & 1][1] = rt.t_frag(ql, (x + 1) >> 1, 2 * j + ((x + 1) & 1));
+        }
+        mfma_acc(dva[x >> 1], ft[x & 1][0], pf[x & 1]);
+        mfma_acc(dka[x >> 1], ft[x & 1][1], sf[x & 1]);
       }
-      dva[x / NC] = E::mma(ft[x & 1][0], pf[x % NC], dva[x / NC]);
-      dka[x / NC] = E::mma(ft[x & 1][1], sf[x % NC], dka[x / NC]);
     }
   };
 
@@ -460,13 +477,17 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
       const char* dl_ = lds + (2 + buf) * TILE;
       const float* lsel = reinterpret_cast<const float*>(lds + 4 * TILE + buf * STAT);
       const float* dltl = reinterpret_cast<const float*>(lds + 4 * TILE + (2 + buf) * STAT);
-      if (masked) tile(hq, qbase, ql, dl_, lsel, dltl, std::true_type{});
-      else tile(hq, qbase, ql, dl_, lsel, dltl, std::false_type{});
+      tile(hq, qbase, ql, dl_, lsel, dltl, masked);
     }
     wait_vmem();
     __syncthreads();
   }
 
+#pragma unroll
+  for (int i = 0; i < DT; ++i) {
+    mfma_drain(dka[i]);
+    mfma_drain(dva[i]);
+  }
   if (kvalid) {
     uint16_t* dkp = static_cast<uint16_t*>(a.dk) + ((size_t)head * P.Skv + kw) * D;
     uint16_t* dvp = static_cast<uint16_t*>(a.dv) + ((size_t)head * P.Skv + kw) * D;

@@ -74,6 +74,26 @@ constexpr int kSchedDsRead = 0x100;
 constexpr int kSchedDsWrite = 0x200;
 constexpr int kSchedValu = 0x002;
 
+// ---- accumulate-in-place MFMA ---------------------------------------------
+// acc += A * B (v_mfma_f32_32x32x16_bf16) with acc pinned to AGPRs and tied
+// in place.  Used for accumulators that only MFMAs touch inside a loop (dQ,
+// dK, dV): the builtin's VGPR form picks a fresh destination and copies it
+// back every iteration.  Inline asm is opaque to the compiler's hazard
+// recognizer, so the wait states the ISA requires are explicit:
+//   * a VALU write of A or B needs 2 wait states before an MFMA reads it:
+//     every call starts with s_nop 1;
+//   * an MFMA result (8-pass XDL) needs up to 12 wait states before another
+//     unit reads it: mfma_drain() after the last accumulation;
+//   * back-to-back accumulation into the same registers needs none.
+__device__ __forceinline__ void mfma_acc(f32x16& acc, u32x4 a, u32x4 b) {
+  asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+// Orders later reads of acc after 20 wait states (and earlier writes of acc,
+// e.g. zero-initialisation, before later MFMAs by at least as much).
+__device__ __forceinline__ void mfma_drain(f32x16& acc) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+a"(acc));
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
