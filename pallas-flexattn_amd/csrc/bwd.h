@@ -65,6 +65,7 @@ struct QWalk {
   const Problem* P;
   int b, hq0, g, kvrow, sub, bq, ntiles_dense;
   bool dense;
+  int n_full, n_all;  // set by init()
   __device__ __forceinline__ void head_lists(int hq, int* nf, const int** fl, int* np, const int** pl) const {
     const int row = tab_row(*P, b, hq, kvrow, P->n_kvblk);
     *nf = P->full_q_num ? clamp_count(scalar_load(P->full_q_num, row), P->q_width) : 0;
@@ -72,45 +73,83 @@ struct QWalk {
     *np = P->q_num ? clamp_count(scalar_load(P->q_num, row), P->q_width) : 0;
     *pl = P->q_num ? P->q_idx + (size_t)row * P->q_width : nullptr;
   }
-  __device__ __forceinline__ int per_head(int hq) const {
-    if (dense) return ntiles_dense;
+  // tiles of head hq in the full (part = 0) or partial (part = 1) list
+  __device__ __forceinline__ int per_head(int hq, int part) const {
+    if (dense) return (part == (P->has_mask ? 1 : 0)) ? ntiles_dense : 0;
     int nf, np;
     const int *fl, *pl;
     head_lists(hq, &nf, &fl, &np, &pl);
-    return (nf + np) * sub;
+    return (part ? np : nf) * sub;
   }
-  __device__ __forceinline__ int count() const {
-    if (dense || P->tab_h == 1) return g * per_head(hq0);
+  __device__ __forceinline__ int count_part(int part) const {
+    if (dense || P->tab_h == 1) return g * per_head(hq0, part);
     int n = 0;
-    for (int i = 0; i < g; ++i) n += per_head(hq0 + i);
+    for (int i = 0; i < g; ++i) n += per_head(hq0 + i, part);
     return n;
+  }
+  // Iteration order: the full tiles of every head of the group, then the
+  // partial ones, so a kernel can run the two kinds in separate loops.
+  __device__ __forceinline__ void init() {
+    n_full = count_part(0);
+    n_all = n_full + count_part(1);
+  }
+  __device__ __forceinline__ int count() const { return n_all; }
+  __device__ __forceinline__ int count_full() const { return n_full; }
+  __device__ __forceinline__ TileRef fetch(int it) const {
+    const int part = it >= n_full ? 1 : 0;
+    int gi = 0, rem = part ? it - n_full : it;
+    if (dense || P->tab_h == 1) {
+      const int c = per_head(hq0, part);
+      gi = c > 0 ? rem / c : 0;
+      rem -= gi * c;
+    } else {
+      for (; gi < g - 1; ++gi) {
+        const int c = per_head(hq0 + gi, part);
+        if (rem < c) break;
+        rem -= c;
+      }
+    }
+    TileRef r{rem, 0, hq0 + gi};
+    if (!dense) {
+      int nf, np;
+      const int *fl, *pl;
+      head_lists(r.hq, &nf, &fl, &np, &pl);
+      const int bi = rem / sub;
+      r.s = rem - bi * sub;
+      r.raw = part ? scalar_load(pl, bi) : scalar_load(fl, bi);
+    }
+    return r;
+  }
+  __device__ __forceinline__ int qbase(const TileRef& r) const {
+    if (dense) return r.raw * bq;
+    return (r.raw < 0 || r.raw >= P->n_qblk) ? kPastEnd : r.raw * P->mblk_q + r.s * bq;
   }
   // -> q head, first query of the tile, whether the element mask applies
   __device__ __forceinline__ void get(int it, int* hq, int* qbase, bool* masked) const {
-    int gi = 0, rem = it;
+    const int part = it >= n_full ? 1 : 0;
+    int gi = 0, rem = part ? it - n_full : it;
     if (dense || P->tab_h == 1) {
-      const int c = per_head(hq0);
-      gi = it / c;
-      rem = it - gi * c;
+      const int c = per_head(hq0, part);
+      gi = c > 0 ? rem / c : 0;
+      rem -= gi * c;
     } else {
       for (; gi < g - 1; ++gi) {
-        const int c = per_head(hq0 + gi);
+        const int c = per_head(hq0 + gi, part);
         if (rem < c) break;
         rem -= c;
       }
     }
     *hq = hq0 + gi;
+    *masked = part != 0;
     if (dense) {
       *qbase = rem * bq;
-      *masked = P->has_mask;
       return;
     }
     int nf, np;
     const int *fl, *pl;
     head_lists(*hq, &nf, &fl, &np, &pl);
     const int bi = rem / sub, s = rem - bi * sub;
-    const int idx = bi < nf ? scalar_load(fl, bi) : scalar_load(pl, bi - nf);
-    *masked = bi >= nf;
+    const int idx = part ? scalar_load(pl, bi) : scalar_load(fl, bi);
     *qbase = (idx < 0 || idx >= P->n_qblk) ? kPastEnd : idx * P->mblk_q + s * bq;
   }
 };
@@ -173,6 +212,7 @@ __global__ __launch_bounds__(NW * 64) void dkdv_kernel(BwdArgs a) {
   walk.bq = BQ;
   walk.dense = !P.has_tables;
   walk.ntiles_dense = (P.Sq + BQ - 1) / BQ;
+  walk.init();
   const int n_it = walk.count();
 
   u32x4 qst[GLOADS][4], dst[GLOADS][4];

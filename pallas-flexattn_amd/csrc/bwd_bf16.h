@@ -8,7 +8,7 @@
 //   * transposed, "column d, eight consecutive rows" (two ds_read_b64_tr_b16),
 //     for the products that contract over the tile's rows (K^T in dQ, Q^T and
 //     dO^T in dK/dV) — no transposed copy is ever written.
-// Chunk c (16 bytes) of row r sits in slot c ^ ((r + 4*(r>>3)) & 7), which keeps
+// Chunk c (16 bytes) of row r sits in slot c ^ chunk_swz(r), which keeps
 // both access patterns free of bank conflicts.  Every MFMA phase fetches the
 // operands of step k+1 before issuing the MFMAs of step k.
 //
@@ -27,19 +27,30 @@
 #include "bwd.h"
 #include "dma.h"
 
+#ifndef FA_DKDV_FAST
+#define FA_DKDV_FAST 1
+#endif
+#ifndef FA_DKDV_APF
+#define FA_DKDV_APF 2
+#endif
+#ifndef FA_DKDV_CPF
+#define FA_DKDV_CPF 2
+#endif
+
 namespace fa {
 
-// Lane-constant LDS offsets for reading a swizzled row-major bf16 tile.
+// Lane-constant LDS offsets for reading a swizzled row-major bf16 tile
+// (chunk c of row r in slot c ^ chunk_swz(r)).
 template <int D>
 struct RowTile {
   static constexpr int RB = D * 2;
   static constexpr int KCH = D / 8;
   static constexpr int KSTEPS = D / 16;
-  static constexpr int MASK = (KCH >= 8 ? 8 : KCH) - 1;
-  __device__ static __forceinline__ int swz(int r) { return (r + 4 * (r >> 3)) & MASK; }
+  static constexpr int DT = D / 32;
+  __device__ static __forceinline__ int swz(int r) { return chunk_swz<KCH>(r); }
 
   int aoff[KSTEPS];  // A operand, rows perm23(lane%32) (+32j), k step s
-  int tr[2][2];      // transposing read: [rows +0..3 / +4..7][d-tile parity]
+  int tr[2][DT];     // transposing read: [rows +0..3 / +4..7][d tile]
 
   __device__ __forceinline__ void init(int lane) {
     const int lr = lane & 31, hh = lane >> 5;
@@ -50,23 +61,22 @@ struct RowTile {
     const int rowbase = 8 * (g >> 1) + (s16 >> 2);
     const int x = 2 * (g & 1) + ((s16 & 3) >> 1);
 #pragma unroll
-    for (int rd = 0; rd < 2; ++rd) {
-      const int row = 4 * rd + rowbase;
-      const int z = swz(row);
-      const int base = row * RB + ((x ^ (z & 3)) * 16) + (s16 & 1) * 8;
-      const int zb = (z >> 2) * 64;
-      tr[rd][0] = base + zb;  // even d tiles: bit 2 of the chunk index is flipped by z
-      tr[rd][1] = base - zb;  // odd d tiles
-    }
+    for (int rd = 0; rd < 2; ++rd)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int row = 4 * rd + rowbase;
+        tr[rd][dt] = row * RB + (((4 * dt + x) ^ swz(row)) * 16) + (s16 & 1) * 8;
+      }
   }
   // A operand: rows 32*j + perm23(lane%32), d = 16*s + 8*(lane/32) + [0..7]
   __device__ __forceinline__ u32x4 a_frag(const char* tile, int j, int s) const {
     return *reinterpret_cast<const u32x4*>(tile + j * 32 * RB + aoff[s]);
   }
   // transposed A operand: row d = 32*dt + lane%32, k = tile rows 16*c + 8*(lane/32) + [0..7]
+  // (the swizzle depends on r & 15 only, so rows +16c are a constant offset)
   __device__ __forceinline__ u32x4 t_frag(const char* tile, int dt, int c) const {
-    const uint2 lo = lds_read_tr16(tile + tr[0][dt & 1] + 16 * c * RB + 64 * dt);
-    const uint2 hi = lds_read_tr16(tile + tr[1][dt & 1] + 16 * c * RB + 64 * dt);
+    const uint2 lo = lds_read_tr16(tile + tr[0][dt] + 16 * c * RB);
+    const uint2 hi = lds_read_tr16(tile + tr[1][dt] + 16 * c * RB);
     return u32x4{lo.x, lo.y, hi.x, hi.y};
   }
 };
@@ -97,23 +107,28 @@ struct TileDma {
 };
 
 // acc += A(tileA rows 32j..) * bA[s]  and  acc2 += A(tileB rows 32j..) * bB[s]
-// over all k steps, operands fetched one step ahead.
-template <int D>
+// over all k steps, operands fetched PF steps ahead (one step is two MFMAs,
+// 64 cycles; an LDS read under load takes longer than that).
+template <int D, int PF = 1>
 __device__ __forceinline__ void mma_rows2(const RowTile<D>& rt, const char* ta, const char* tb, int j,
                                           const u32x4* ba, const u32x4* bb, f32x16& acc, f32x16& acc2) {
   using E = Elt<uint16_t>;
   constexpr int KS = D / 16;
-  u32x4 fa[2], fb[2];
-  fa[0] = rt.a_frag(ta, j, 0);
-  fb[0] = rt.a_frag(tb, j, 0);
+  constexpr int R = PF + 1;
+  u32x4 fa[R], fb[R];
+#pragma unroll
+  for (int s = 0; s < PF && s < KS; ++s) {
+    fa[s] = rt.a_frag(ta, j, s);
+    fb[s] = rt.a_frag(tb, j, s);
+  }
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
-    if (s + 1 < KS) {
-      fa[(s + 1) & 1] = rt.a_frag(ta, j, s + 1);
-      fb[(s + 1) & 1] = rt.a_frag(tb, j, s + 1);
+    if (s + PF < KS) {
+      fa[(s + PF) % R] = rt.a_frag(ta, j, s + PF);
+      fb[(s + PF) % R] = rt.a_frag(tb, j, s + PF);
     }
-    acc = E::mma(fa[s & 1], ba[s], acc);
-    acc2 = E::mma(fb[s & 1], bb[s], acc2);
+    acc = E::mma(fa[s % R], ba[s], acc);
+    acc2 = E::mma(fb[s % R], bb[s], acc2);
   }
 }
 
@@ -124,7 +139,7 @@ __device__ __forceinline__ void zero(f32x16& x) {
 
 // ------------------------------------------------------------------- dQ ----
 template <int D, int BN, int NW, bool kMods>
-__global__ __launch_bounds__(NW * 64) void dq_bf16_kernel(BwdArgs a) {
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void dq_bf16_kernel(BwdArgs a) {
   using E = Elt<uint16_t>;
   using frag = E::frag;
   constexpr int BM = 32 * NW;
@@ -199,11 +214,11 @@ __global__ __launch_bounds__(NW * 64) void dq_bf16_kernel(BwdArgs a) {
     dma.issue(vbase_ptr, kb, P.Skv, lds + (2 + buf) * TILE, w);
   };
 
-  f32x16 dqa[DT];  // AGPRs, accumulated in place
+  f32x16 dqa[DT];  // accumulated in place
 #pragma unroll
   for (int i = 0; i < DT; ++i) {
     zero(dqa[i]);
-    mfma_drain(dqa[i]);
+    mfma_drain<'v'>(dqa[i]);
   }
 
   // One kv tile: per 32-key sub-tile S^T, dP^T -> dS^T (packed), then that
@@ -212,7 +227,8 @@ __global__ __launch_bounds__(NW * 64) void dq_bf16_kernel(BwdArgs a) {
   // A single code path for full and partial tiles: only the in-place masking
   // of S^T is conditional, so the loop-carried accumulators keep their
   // registers.
-  auto tile = [&](int kbase, const char* kl, const char* vl, bool masked) {
+  auto tile = [&](int kbase, const char* kl, const char* vl, auto masked_c) {
+    constexpr bool kMasked = decltype(masked_c)::value;
     frag sf[2];
 #pragma unroll
     for (int j = 0; j < NSUB; ++j) {
@@ -227,7 +243,7 @@ __global__ __launch_bounds__(NW * 64) void dq_bf16_kernel(BwdArgs a) {
         if constexpr (kMods)
           sacc[e] = score_t<true>(P, sacc[e], slope, qw, kbase + 32 * j + acc_row(e, hh), &dsdx[e]);
       }
-      if (masked) {
+      if constexpr (kMasked) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int key = kbase + 32 * j + acc_row(e, hh);
@@ -255,37 +271,45 @@ __global__ __launch_bounds__(NW * 64) void dq_bf16_kernel(BwdArgs a) {
 #pragma unroll
       for (int x = 0; x < 2 * DT; ++x) {
         if (x + 1 < 2 * DT) kt[(x + 1) & 1] = rt.t_frag(kl, (x + 1) >> 1, 2 * j + ((x + 1) & 1));
-        mfma_acc(dqa[x >> 1], kt[x & 1], sf[x & 1]);
+        mfma_acc<'v'>(dqa[x >> 1], kt[x & 1], sf[x & 1]);
       }
     }
   };
 
+  // Full tiles run first, in a loop of their own without the element mask;
+  // the partial tiles follow.  Keys past Skv need no mask: their K and V rows
+  // read as zero, so dS K^T gets nothing from them.
+  // Table entries are fetched two tiles ahead, resolved one tile ahead.
   int kb_next = 0;
-  bool msk_next = false;
+  TileRef ref_next{0, 0, 0};
   if (n_it > 0) {
-    walk.get(0, &kb_next, &msk_next);
+    kb_next = walk.kbase(walk.fetch(0));
     issue(kb_next, 0);
-    wait_vmem();
+    if (n_it > 1) ref_next = walk.fetch(1);
   }
+  // unconditional, so the wait-count analysis sees the register loads above
+  // complete on every path into the loop
+  wait_vmem();
   __syncthreads();
-  for (int it = 0; it < n_it; ++it) {
+  auto step = [&](int it, auto masked_c) {
     const int buf = it & 1;
     const int kbase = kb_next;
-    bool masked = msk_next;
     if (it + 1 < n_it) {
-      walk.get(it + 1, &kb_next, &msk_next);
+      kb_next = walk.kbase(ref_next);
       issue(kb_next, buf ^ 1);
     }
-    if (kbase < P.Skv) {
-      masked = masked || (kbase + BN > P.Skv);
-      tile(kbase, lds + buf * TILE, lds + (2 + buf) * TILE, masked);
-    }
+    if (it + 2 < n_it) ref_next = walk.fetch(it + 2);
+    if (kbase < P.Skv) tile(kbase, lds + buf * TILE, lds + (2 + buf) * TILE, masked_c);
     wait_vmem();
     __syncthreads();
-  }
+  };
+  const int n_full = walk.count_full();
+  int it = 0;
+  for (; it < n_full; ++it) step(it, std::false_type{});
+  for (; it < n_it; ++it) step(it, std::true_type{});
 
 #pragma unroll
-  for (int i = 0; i < DT; ++i) mfma_drain(dqa[i]);
+  for (int i = 0; i < DT; ++i) mfma_drain<'v'>(dqa[i]);
   if (qvalid) {
     uint16_t* dqp = static_cast<uint16_t*>(a.dq) + rowi * D;
 #pragma unroll
@@ -313,6 +337,7 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   constexpr int NC = BQ / 16;
   constexpr int TILE = BQ * RB;
   constexpr int STAT = 1024;  // LSE / Delta landing zone per buffer (BQ floats used)
+  constexpr int APF = FA_DKDV_APF, CPF = FA_DKDV_CPF;  // operand prefetch depths (steps)
   static_assert(BQ * 4 <= STAT, "stat tile");
   __shared__ __attribute__((aligned(1024))) char lds[4 * TILE + 4 * STAT];  // Q0 Q1 dO0 dO1 L0 L1 D0 D1
 
@@ -356,6 +381,7 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   walk.bq = BQ;
   walk.dense = !P.has_tables;
   walk.ntiles_dense = (P.Sq + BQ - 1) / BQ;
+  walk.init();
   const int n_it = walk.count();
 
   auto issue = [&](int hq, int qb, int buf) {
@@ -377,8 +403,8 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   for (int i = 0; i < DT; ++i) {  // AGPRs, accumulated in place
     zero(dka[i]);
     zero(dva[i]);
-    mfma_drain(dka[i]);
-    mfma_drain(dva[i]);
+    mfma_drain<'a'>(dka[i]);
+    mfma_drain<'a'>(dva[i]);
   }
 
   // One q tile, one code path for full and partial tiles (only the in-place
@@ -387,14 +413,15 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   // share of dV^T += dO^T P and dK^T += Q^T dS (transposed fragments one step
   // ahead), so the next sub-tile's MFMAs can overlap this one's exponentials.
   auto tile = [&](int hq, int qbase, const char* ql, const char* dl_, const float* lsel, const float* dltl,
-                  bool masked) {
+                  auto masked_c) {
+    constexpr bool kMasked = decltype(masked_c)::value;
     const float slope = P.alibi ? P.alibi[hq] : 0.f;
 #pragma unroll
     for (int j = 0; j < NQS; ++j) {
       f32x16 sacc, pacc;
       zero(sacc);
       zero(pacc);
-      mma_rows2<D>(rt, ql, dl_, j, kf, vf, sacc, pacc);
+      mma_rows2<D, APF>(rt, ql, dl_, j, kf, vf, sacc, pacc);
       float dsdx[16];
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
@@ -404,7 +431,7 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
           sacc[e] = score_t<true>(P, sacc[e], slope, qi, kw, &dsdx[e]);
         }
       }
-      if (masked) {
+      if constexpr (kMasked) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int qi = qbase + 32 * j + acc_row(e, hh);
@@ -439,54 +466,158 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
         pf[half] = E::pack(x);
         sf[half] = E::pack(y);
       }
-      // x = (d tile, chunk half) of this sub-tile: chunk c = 2j + half
-      frag ft[2][2];
-      ft[0][0] = rt.t_frag(dl_, 0, 2 * j);
-      ft[0][1] = rt.t_frag(ql, 0, 2 * j);
+      // x = (d tile, chunk half) of this sub-tile: chunk c = 2j + half;
+      // transposed fragments fetched CPF steps ahead
+      constexpr int CR = CPF + 1;
+      frag ft[CR][2];
+#pragma unroll
+      for (int x = 0; x < CPF; ++x) {
+        ft[x][0] = rt.t_frag(dl_, x >> 1, 2 * j + (x & 1));
+        ft[x][1] = rt.t_frag(ql, x >> 1, 2 * j + (x & 1));
+      }
 #pragma unroll
       for (int x = 0; x < 2 * DT; ++x) {
-        if (x + 1 < 2 * DT) {
-          ft[(x + 1) & 1][0] = rt.t_frag(dl_, (x + 1) >> 1, 2 * j + ((x + 1) & 1));
-          ft[(x + 1) & 1][1] = rt.t_frag(ql, (x + 1) >> 1, 2 * j + ((x + 1) & 1));
+        if (x + CPF < 2 * DT) {
+          ft[(x + CPF) % CR][0] = rt.t_frag(dl_, (x + CPF) >> 1, 2 * j + ((x + CPF) & 1));
+          ft[(x + CPF) % CR][1] = rt.t_frag(ql, (x + CPF) >> 1, 2 * j + ((x + CPF) & 1));
         }
-        mfma_acc(dva[x >> 1], ft[x & 1][0], pf[x & 1]);
-        mfma_acc(dka[x >> 1], ft[x & 1][1], sf[x & 1]);
+        mfma_acc<'a'>(dva[x >> 1], ft[x % CR][0], pf[x & 1]);
+        mfma_acc<'a'>(dka[x >> 1], ft[x % CR][1], sf[x & 1]);
       }
     }
   };
 
+  // Full tiles without score mods: the q tile is a fixed sequence of 4*KS
+  // steps of two MFMAs each, in four phases
+  //   A0: S_0, dP_0  |  A1: S_1, dP_1  |  C0: dV^T, dK^T += (sub-tile 0)  |  C1
+  // with the exponentials / dS of sub-tile 0 (E0) spread over A1's steps and
+  // those of sub-tile 1 (E1) over C0's, so VALU work issues while the matrix
+  // core is busy.  Every step also fetches the LDS operands of the step PF
+  // ahead (across phase boundaries; row fragments in A, transposed ones in C)
+  // and the LSE / Delta of the E quad due next.  sched_barrier fences keep
+  // the compiler to this order.
+  auto tile_fast = [&](const char* ql, const char* dl_, const float* lsel, const float* dltl) {
+    constexpr int KS = KSTEPS, NSTEP = 4 * KS, PF = APF, R = PF + 1;
+    static_assert(2 * DT == KS && NQS == 2, "fast path shape");
+    // step of phase 1 / 2 at which E quad q is computed
+    auto quad_step = [](int q) { int s = (q + 1) * KS / 4 - 1; return s < 0 ? 0 : s; };
+    f32x16 sacc[2], pacc[2];
+    zero(sacc[0]); zero(pacc[0]); zero(sacc[1]); zero(pacc[1]);
+    frag pf[2][2], sf[2][2];
+    frag ring[R][2];
+    f32x4 ls[2][4], dd[2][4];
+    auto load = [&](int t) {
+      const int ph = t / KS, s = t % KS;
+      if (ph < 2) {
+        ring[t % R][0] = rt.a_frag(ql, ph, s);
+        ring[t % R][1] = rt.a_frag(dl_, ph, s);
+      } else {
+        const int j = ph - 2;
+        ring[t % R][0] = rt.t_frag(dl_, s >> 1, 2 * j + (s & 1));
+        ring[t % R][1] = rt.t_frag(ql, s >> 1, 2 * j + (s & 1));
+      }
+    };
+    auto load_stats = [&](int j, int q) {
+      const int r0 = 32 * j + acc_row(4 * q, hh);
+      ls[j][q] = *reinterpret_cast<const f32x4*>(lsel + r0);
+      dd[j][q] = *reinterpret_cast<const f32x4*>(dltl + r0);
+    };
+    auto equad = [&](int j, int q) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = 4 * q + i;
+        const float pv = fast_exp2(fmaf(sacc[j][e], P.scale_log2, -ls[j][q][i] * kLog2e));
+        sacc[j][e] = pv;
+        pacc[j][e] = pv * (pacc[j][e] - dd[j][q][i]);
+      }
+      if (q & 1) {
+        const int half = q >> 1;
+        float x[8], y[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          x[t] = sacc[j][8 * half + t];
+          y[t] = pacc[j][8 * half + t];
+        }
+        pf[j][half] = E::pack(x);
+        sf[j][half] = E::pack(y);
+      }
+    };
+#pragma unroll
+    for (int t = 0; t < PF; ++t) load(t);
+#pragma unroll
+    for (int t = 0; t < NSTEP; ++t) {
+      const int ph = t / KS, s = t % KS;
+      if (t + PF < NSTEP) load(t + PF);
+      // stats of the E quads computed in the next step
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          if ((j + 1) * KS + quad_step(q) == t + 1) load_stats(j, q);
+      if (ph < 2) {
+        sacc[ph] = E::mma(ring[t % R][0], kf[s], sacc[ph]);
+        pacc[ph] = E::mma(ring[t % R][1], vf[s], pacc[ph]);
+      } else {
+        const int j = ph - 2;
+        mfma_acc<'a'>(dva[s >> 1], ring[t % R][0], pf[j][s & 1]);
+        mfma_acc<'a'>(dka[s >> 1], ring[t % R][1], sf[j][s & 1]);
+      }
+      if (ph == 1 || ph == 2) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (quad_step(q) == s) equad(ph - 1, q);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // Full tiles run first, in a loop of their own without the element mask;
+  // the partial tiles follow.  Rows past Sq need no mask: their Q, dO, LSE and
+  // Delta read as zero, so P = 1 and dS = 0 there and dO^T P, Q^T dS get
+  // nothing from them.  Keys past Skv only touch lanes that are not stored.
+  // Table entries are fetched two tiles ahead, resolved one tile ahead.
   int hq_next = 0, qb_next = 0;
-  bool msk_next = false;
+  TileRef ref_next{0, 0, 0};
   if (n_it > 0) {
-    walk.get(0, &hq_next, &qb_next, &msk_next);
+    const TileRef r0 = walk.fetch(0);
+    hq_next = r0.hq;
+    qb_next = walk.qbase(r0);
     issue(hq_next, qb_next, 0);
-    wait_vmem();
+    if (n_it > 1) ref_next = walk.fetch(1);
   }
+  // unconditional, so the wait-count analysis sees the register loads above
+  // complete on every path into the loop
+  wait_vmem();
   __syncthreads();
-  for (int it = 0; it < n_it; ++it) {
+  auto step = [&](int it, auto masked_c) {
     const int buf = it & 1;
     const int hq = hq_next, qbase = qb_next;
-    bool masked = msk_next;
     if (it + 1 < n_it) {
-      walk.get(it + 1, &hq_next, &qb_next, &msk_next);
+      hq_next = ref_next.hq;
+      qb_next = walk.qbase(ref_next);
       issue(hq_next, qb_next, buf ^ 1);
     }
+    if (it + 2 < n_it) ref_next = walk.fetch(it + 2);
     if (qbase < P.Sq) {
-      masked = masked || (k0 + BKV > P.Skv) || (qbase + BQ > P.Sq);
-      const char* ql = lds + buf * TILE;
-      const char* dl_ = lds + (2 + buf) * TILE;
       const float* lsel = reinterpret_cast<const float*>(lds + 4 * TILE + buf * STAT);
       const float* dltl = reinterpret_cast<const float*>(lds + 4 * TILE + (2 + buf) * STAT);
-      tile(hq, qbase, ql, dl_, lsel, dltl, masked);
+      if constexpr (!decltype(masked_c)::value && !kMods && FA_DKDV_FAST)
+        tile_fast(lds + buf * TILE, lds + (2 + buf) * TILE, lsel, dltl);
+      else
+        tile(hq, qbase, lds + buf * TILE, lds + (2 + buf) * TILE, lsel, dltl, masked_c);
     }
     wait_vmem();
     __syncthreads();
-  }
+  };
+  const int n_full = walk.count_full();
+  int it = 0;
+  for (; it < n_full; ++it) step(it, std::false_type{});
+  for (; it < n_it; ++it) step(it, std::true_type{});
 
 #pragma unroll
   for (int i = 0; i < DT; ++i) {
-    mfma_drain(dka[i]);
-    mfma_drain(dva[i]);
+    mfma_drain<'a'>(dka[i]);
+    mfma_drain<'a'>(dva[i]);
   }
   if (kvalid) {
     uint16_t* dkp = static_cast<uint16_t*>(a.dk) + ((size_t)head * P.Skv + kw) * D;

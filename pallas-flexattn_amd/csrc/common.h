@@ -61,6 +61,37 @@ __device__ __forceinline__ float pair_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// ---- LDS tile swizzle ------------------------------------------------------
+// Row-major bf16 tiles with KCH 16-byte chunks per row store logical chunk c
+// of row r in slot c ^ chunk_swz<KCH>(r).  gfx950's LDS serves 64 banks x 4 B
+// per clock: a ds_read_b128 is conflict-free when each group of 16 lanes
+// covers 16 distinct 16-byte bank slots, a ds_read_b64_tr_b16 when each group
+// of 32 lanes (4 rows x 4 chunks) does.  With KCH = 16 (one row per 256-byte
+// bank row) the swizzle maps
+//   * the 16 rows an A-operand read takes (any 16-aligned row block, same
+//     logical chunk) to 16 distinct slots: f is a bijection on r & 15;
+//   * the 4 consecutive rows of a transposing read to 4 distinct quarter-rows:
+//     bits 2-3 of f are r & 3.
+// KCH = 8 and 4 (two / four rows per bank row) follow the same rules with the
+// row's position in the bank row taking the place of the high bits.
+template <int KCH>
+__device__ __forceinline__ int chunk_swz(int r) {
+  static_assert(KCH == 4 || KCH == 8 || KCH == 16, "chunks per row");
+  if constexpr (KCH == 16) return ((r & 3) << 2) | ((r >> 2) & 3);
+  else if constexpr (KCH == 8) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+  else return (r >> 2) & 3;
+}
+
+// Swizzle for tiles read only by transposing reads (the forward's V): the 4
+// rows of a read land in distinct quarter-rows and rows r, r + 4 share their
+// swizzle, so a lane's addresses for rows +0..3 and +4..7 differ by a constant.
+template <int KCH>
+__device__ __forceinline__ int tr_swz(int r) {
+  if constexpr (KCH == 16) return 4 * (r & 3);
+  else if constexpr (KCH == 8) return 4 * ((r >> 1) & 1);
+  else return 0;
+}
+
 // Load through the scalar data cache (the address must be wave-uniform).
 __device__ __forceinline__ int scalar_load(const int* p, int i) {
   typedef const __attribute__((address_space(4))) int* cptr;
@@ -75,23 +106,32 @@ constexpr int kSchedDsWrite = 0x200;
 constexpr int kSchedValu = 0x002;
 
 // ---- accumulate-in-place MFMA ---------------------------------------------
-// acc += A * B (v_mfma_f32_32x32x16_bf16) with acc pinned to AGPRs and tied
-// in place.  Used for accumulators that only MFMAs touch inside a loop (dQ,
-// dK, dV): the builtin's VGPR form picks a fresh destination and copies it
-// back every iteration.  Inline asm is opaque to the compiler's hazard
-// recognizer, so the wait states the ISA requires are explicit:
+// acc += A * B (v_mfma_f32_32x32x16_bf16) with acc tied in place, in AGPRs
+// (kReg = 'a') or VGPRs ('v').  Used for accumulators that only MFMAs touch
+// inside a loop (dQ, dK, dV): the builtin's VGPR form picks a fresh
+// destination and copies it back every iteration.  Inline asm is opaque to
+// the compiler's hazard recognizer, so the wait states the ISA requires are
+// explicit:
 //   * a VALU write of A or B needs 2 wait states before an MFMA reads it:
 //     every call starts with s_nop 1;
 //   * an MFMA result (8-pass XDL) needs up to 12 wait states before another
 //     unit reads it: mfma_drain() after the last accumulation;
 //   * back-to-back accumulation into the same registers needs none.
+template <char kReg>
 __device__ __forceinline__ void mfma_acc(f32x16& acc, u32x4 a, u32x4 b) {
-  asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+  if constexpr (kReg == 'a')
+    asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+  else
+    asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
 }
 // Orders later reads of acc after 20 wait states (and earlier writes of acc,
 // e.g. zero-initialisation, before later MFMAs by at least as much).
+template <char kReg>
 __device__ __forceinline__ void mfma_drain(f32x16& acc) {
-  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+a"(acc));
+  if constexpr (kReg == 'a')
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+a"(acc));
+  else
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(acc));
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

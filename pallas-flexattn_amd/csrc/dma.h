@@ -31,11 +31,34 @@ __device__ __forceinline__ u32x4 buf_load16(i32x4 rsrc, int byte_off) {
 
 // Copy 16 bytes per lane from the buffer at byte_off into LDS at
 // lds_wave_base + 16 * lane (lds_wave_base must be wave-uniform).
+//
+// Issued as inline asm on purpose: for the intrinsic form the compiler tracks
+// the asynchronous LDS write and, unable to tell the next tile's buffer from
+// the current one, puts an s_waitcnt vmcnt(0) before LDS reads it cannot
+// disambiguate (the transposing reads), so every tile would wait for the
+// next tile's copy.  Callers make the data visible themselves: wait_vmem()
+// and a workgroup barrier before any wave reads the tile.  The compiler's own
+// vmcnt waits stay correct: loads counted in order only complete later when
+// unknown copies are queued behind them.
 __device__ __forceinline__ void dma16(i32x4 rsrc, int byte_off, char* lds_wave_base) {
-  raw_buffer_load_lds(rsrc, (FA_LDS uint32_t*)(lds_wave_base), 16, byte_off, 0, 0, 0);
+  // the low 32 bits of a flat pointer into the shared aperture are the LDS
+  // byte address
+  const uint32_t m0v = __builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)lds_wave_base);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(byte_off), "s"(rsrc), "s"(m0v)
+               : "memory", "m0");
 }
 
-__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// s_waitcnt vmcnt(0) (expcnt, lgkmcnt left at their maxima) through the
+// builtin, so the compiler's own wait insertion knows that every earlier
+// vector-memory load has completed; the empty asm keeps memory accesses from
+// moving across it.
+__device__ __forceinline__ void wait_vmem() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  asm volatile("" ::: "memory");
+}
 
 // ds_read_b64_tr_b16: within each group of 16 lanes, source lane s supplies the
 // address of 4 consecutive 16-bit elements (row s/4 of a 4x16 block at column

@@ -26,6 +26,15 @@ struct FwdArgs {
   float* lse;  // (B, Hq, Sq), natural-log units
 };
 
+// A tile of a walk whose table entry may still be in flight: fetch() issues
+// the scalar load, the walk's resolve step turns the entry into a tile start
+// (an iteration or two later, so the load latency is hidden).
+struct TileRef {
+  int raw;  // table entry (dense walks: the tile number)
+  int s;    // sub-tile of the mask block
+  int hq;   // q head (q-side walks)
+};
+
 // kv-tile iteration over block tables (or densely over all tiles)
 struct KvWalk {
   const int* full;
@@ -33,6 +42,23 @@ struct KvWalk {
   int nfull, npart, sub, bn, mblk, nblk, ntiles_dense;
   bool dense, dense_masked;
   __device__ __forceinline__ int count() const { return dense ? ntiles_dense : (nfull + npart) * sub; }
+  // the full tiles come first in the iteration order
+  __device__ __forceinline__ int count_full() const {
+    return dense ? (dense_masked ? 0 : ntiles_dense) : nfull * sub;
+  }
+  __device__ __forceinline__ TileRef fetch(int it) const {
+    TileRef r{it, 0, 0};
+    if (!dense) {
+      const int bi = it / sub;
+      r.s = it - bi * sub;
+      r.raw = bi < nfull ? scalar_load(full, bi) : scalar_load(part, bi - nfull);
+    }
+    return r;
+  }
+  __device__ __forceinline__ int kbase(const TileRef& r) const {
+    if (dense) return r.raw * bn;
+    return (r.raw < 0 || r.raw >= nblk) ? kPastEnd : r.raw * mblk + r.s * bn;
+  }
   __device__ __forceinline__ void get(int it, int* kbase, bool* masked) const {
     if (dense) {
       *kbase = it * bn;

@@ -19,9 +19,9 @@
 //   * O^T += V^T P^T (A = V^T fetched from the row-major V tile with
 //     ds_read_b64_tr_b16, B = P^T straight from the S^T accumulators).
 // LDS layouts (row = key, 16-byte chunks): K chunk c of row r sits in slot
-// c ^ ((r + 4*(r>>3)) & 7) — the 32 rows read together by an A-operand load
-// land in distinct banks; V chunk c sits in slot c ^ (r & 3) — the 4
-// consecutive rows of one transposing read land in distinct banks.
+// c ^ chunk_swz(r) — each 16 lanes of an A-operand load hit 16 distinct bank
+// slots; V chunk c sits in slot c ^ tr_swz(r) — the 4 consecutive rows of one
+// transposing read land in distinct quarter-rows.
 #pragma once
 #include <type_traits>
 
@@ -43,7 +43,6 @@ void fwd_bf16_kernel(FwdArgs a) {
   constexpr int DT = D / 32;
   constexpr int TILE = BN * RB;         // bytes per K (or V) tile
   constexpr int IPW = TILE / 1024 / NW; // DMA instructions per wave per tile
-  constexpr int KMASK = (KCH >= 8 ? 8 : KCH) - 1;
   static_assert(KCH >= 4 && D % 32 == 0 && BN % 32 == 0, "tile shape");
   static_assert(TILE % (1024 * NW) == 0, "DMA split");
 
@@ -83,21 +82,24 @@ void fwd_bf16_kernel(FwdArgs a) {
   for (int u = 0; u < IPW; ++u) {
     const int g = (w * IPW + u) * 64 + lane;
     const int r = g / KCH, p = g % KCH;
-    dma_off_k[u] = r * RB + ((p ^ ((r + 4 * (r >> 3)) & KMASK)) * 16);
-    dma_off_v[u] = r * RB + ((p ^ (r & 3)) * 16);
+    dma_off_k[u] = r * RB + ((p ^ chunk_swz<KCH>(r)) * 16);
+    dma_off_v[u] = r * RB + ((p ^ tr_swz<KCH>(r)) * 16);
   }
   int koffA[KSTEPS];
   {
     const int r = perm23(lr);
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) koffA[s] = r * RB + (((2 * s + hh) ^ ((r + 4 * (r >> 3)) & KMASK)) * 16);
+    for (int s = 0; s < KSTEPS; ++s) koffA[s] = r * RB + (((2 * s + hh) ^ chunk_swz<KCH>(r)) * 16);
   }
-  int voffT;
+  // transposing reads of V: rows row + 16c (+4 for the upper half of the
+  // fragment), chunk 4i + x of d tile i
+  int voffT[DT];
   {
     const int s16 = lane & 15, g = lane >> 4;
     const int row = 8 * (g >> 1) + (s16 >> 2);
-    const int chunk = 2 * (g & 1) + ((s16 & 3) >> 1);
-    voffT = row * RB + ((chunk ^ (row & 3)) * 16) + (s16 & 1) * 8;
+    const int x = 2 * (g & 1) + ((s16 & 3) >> 1);
+#pragma unroll
+    for (int i = 0; i < DT; ++i) voffT[i] = row * RB + (((4 * i + x) ^ tr_swz<KCH>(row)) * 16) + (s16 & 1) * 8;
   }
 
   KvWalk walk;
@@ -186,22 +188,29 @@ void fwd_bf16_kernel(FwdArgs a) {
     l += rs;
   };
 
+  // Table entries are fetched two tiles ahead, resolved one tile ahead; the
+  // full tiles come first in the walk.
+  const int n_full = walk.count_full();
   int kb_next = 0;
-  bool msk_next = false;
+  TileRef ref_next{0, 0, 0};
   if (n_it > 0) {
-    walk.get(0, &kb_next, &msk_next);
+    kb_next = walk.kbase(walk.fetch(0));
     issue(kb_next, 0);
-    wait_vmem();
+    if (n_it > 1) ref_next = walk.fetch(1);
   }
+  // unconditional, so the wait-count analysis sees the register loads above
+  // complete on every path into the loop
+  wait_vmem();
   __syncthreads();
   for (int it = 0; it < n_it; ++it) {
     const int buf = it & 1;
     const int kbase = kb_next;
-    bool masked = msk_next;
+    bool masked = it >= n_full;
     if (it + 1 < n_it) {
-      walk.get(it + 1, &kb_next, &msk_next);
+      kb_next = walk.kbase(ref_next);
       issue(kb_next, buf ^ 1);
     }
+    if (it + 2 < n_it) ref_next = walk.fetch(it + 2);
     if (kbase < P.Skv) {  // workgroup-uniform
       masked = masked || (kbase + BN > P.Skv);
       const char* kl = lds + buf * TILE;
@@ -256,8 +265,8 @@ void fwd_bf16_kernel(FwdArgs a) {
       for (int i = 0; i < DT; ++i)
 #pragma unroll
         for (int c = 0; c < BN / 16; ++c) {
-          const uint2 lo = lds_read_tr16(vl + voffT + (16 * c) * RB + 64 * i);
-          const uint2 hi = lds_read_tr16(vl + voffT + (16 * c + 4) * RB + 64 * i);
+          const uint2 lo = lds_read_tr16(vl + voffT[i] + (16 * c) * RB);
+          const uint2 hi = lds_read_tr16(vl + voffT[i] + (16 * c + 4) * RB);
           const frag vf = u32x4{lo.x, lo.y, hi.x, hi.y};
           oacc[i] = E::mma(vf, pf[c], oacc[i]);
         }
