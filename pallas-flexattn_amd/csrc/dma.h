@@ -25,6 +25,17 @@ __device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
   return r;
 }
 
+__device__ int raw_buffer_load_b32(i32x4 rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.i32");
+
+// Element i of an int array of n elements through the vector memory path
+// (zero past the end).  Used for block-table entries inside tile loops: the
+// load completes by the loop's end-of-tile vmcnt wait, whereas a scalar load
+// shares lgkmcnt with the LDS reads and stalls the first LDS wait after it.
+__device__ __forceinline__ int vload_i32(const int* base, int i, int n) {
+  return raw_buffer_load_b32(make_rsrc(base, (uint32_t)n * 4u), i * 4, 0, 0);
+}
+
 __device__ __forceinline__ u32x4 buf_load16(i32x4 rsrc, int byte_off) {
   return __builtin_bit_cast(u32x4, raw_buffer_load_b128(rsrc, byte_off, 0, 0));
 }

@@ -13,6 +13,7 @@
 // The kv loop walks the block tables: fully-live blocks first (no element
 // mask), then partial blocks (mask evaluated per element).
 #pragma once
+#include "dma.h"
 #include "kargs.h"
 
 namespace fa {
@@ -30,10 +31,13 @@ struct FwdArgs {
 // the scalar load, the walk's resolve step turns the entry into a tile start
 // (an iteration or two later, so the load latency is hidden).
 struct TileRef {
-  int raw;  // table entry (dense walks: the tile number)
+  int raw;  // table entry, still in a VGPR (dense walks: the tile number)
   int s;    // sub-tile of the mask block
   int hq;   // q head (q-side walks)
 };
+
+__device__ __forceinline__ int div_pow2_or(int x, int d, int d_log2) { return d_log2 >= 0 ? x >> d_log2 : x / d; }
+__device__ __forceinline__ int log2_if_pow2(int d) { return (d > 0 && (d & (d - 1)) == 0) ? __builtin_ctz(d) : -1; }
 
 // kv-tile iteration over block tables (or densely over all tiles)
 struct KvWalk {
@@ -49,15 +53,16 @@ struct KvWalk {
   __device__ __forceinline__ TileRef fetch(int it) const {
     TileRef r{it, 0, 0};
     if (!dense) {
-      const int bi = it / sub;
+      const int bi = div_pow2_or(it, sub, log2_if_pow2(sub));
       r.s = it - bi * sub;
-      r.raw = bi < nfull ? scalar_load(full, bi) : scalar_load(part, bi - nfull);
+      r.raw = bi < nfull ? vload_i32(full, bi, nfull) : vload_i32(part, bi - nfull, npart);
     }
     return r;
   }
   __device__ __forceinline__ int kbase(const TileRef& r) const {
     if (dense) return r.raw * bn;
-    return (r.raw < 0 || r.raw >= nblk) ? kPastEnd : r.raw * mblk + r.s * bn;
+    const int raw = __builtin_amdgcn_readfirstlane(r.raw);
+    return (raw < 0 || raw >= nblk) ? kPastEnd : raw * mblk + r.s * bn;
   }
   __device__ __forceinline__ void get(int it, int* kbase, bool* masked) const {
     if (dense) {
