@@ -97,12 +97,20 @@ struct TileDma {
       off[u] = r * RB + ((p ^ RowTile<D>::swz(r)) * 16);
     }
   }
-  // rows [row0, row0 + R) of a tensor with `rows` rows starting at `base`
-  __device__ __forceinline__ void issue(const char* base, int row0, int rows, char* lds_tile, int w) const {
+  // resource for rows [row0, row0 + R) of a tensor with `rows` rows at `base`
+  // (rows past the end read as zero; row0 >= rows copies zeros)
+  __device__ __forceinline__ static i32x4 rsrc(const char* base, int row0, int rows) {
     row0 = row0 < rows ? row0 : rows;
-    const i32x4 rs = make_rsrc(base + (size_t)row0 * RB, (uint32_t)(rows - row0) * RB);
+    return make_rsrc(base + (size_t)row0 * RB, (uint32_t)(rows - row0) * RB);
+  }
+  // the u-th of this wave's IPW copy instructions
+  __device__ __forceinline__ void one(const i32x4& rs, int u, char* lds_tile, int w) const {
+    dma16(rs, off[u], lds_tile + (w * IPW + u) * 1024);
+  }
+  __device__ __forceinline__ void issue(const char* base, int row0, int rows, char* lds_tile, int w) const {
+    const i32x4 rs = rsrc(base, row0, rows);
 #pragma unroll
-    for (int u = 0; u < IPW; ++u) dma16(rs, off[u], lds_tile + (w * IPW + u) * 1024);
+    for (int u = 0; u < IPW; ++u) one(rs, u, lds_tile, w);
   }
 };
 
@@ -152,7 +160,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
   __shared__ __attribute__((aligned(1024))) char lds[4 * TILE];  // K0 K1 V0 V1
 
   const Problem& P = a.p;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 31, hh = lane >> 5;
   const int nqt = (P.Sq + BM - 1) / BM;
   int head, qt;
@@ -342,7 +350,7 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[4 * TILE + 4 * STAT];  // Q0 Q1 dO0 dO1 L0 L1 D0 D1
 
   const Problem& P = a.p;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 31, hh = lane >> 5;
   const int nkt = (P.Skv + BKV - 1) / BKV;
   const int g = P.Hq / P.Hkv;
@@ -384,18 +392,38 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   walk.init();
   const int n_it = walk.count();
 
-  auto issue = [&](int hq, int qb, int buf) {
+  // Copies of the next q tile (Q, dO rows, LSE and Delta) into buffer `buf`,
+  // as NDMA single instructions per wave so the fast path can spread them
+  // over its MFMA steps (the texture unit takes one copy instruction at a
+  // time; four waves issuing all of theirs at once after a barrier queue for
+  // hundreds of cycles).  A tile at qb >= Sq copies zeros.
+  // Waves with even index copy the LSE tile, odd ones Delta (each wave one
+  // instruction, no branch; the duplicate writes carry identical data).
+  struct TileCopy {
+    i32x4 rq, rdo, rst;
+    int buf;
+  };
+  constexpr int NDMA = 2 * TileDma<D, BQ, NW>::IPW + 1;
+  auto plan = [&](int hq, int qb, int buf) {
     const size_t hoff = (size_t)(b * P.Hq + hq) * P.Sq;
-    dma.issue(static_cast<const char*>(a.q) + hoff * RB, qb, P.Sq, lds + buf * TILE, w);
-    dma.issue(static_cast<const char*>(a.dout) + hoff * RB, qb, P.Sq, lds + (2 + buf) * TILE, w);
-    if (w == 0) {
-      const int q = qb < P.Sq ? qb : P.Sq;
-      const uint32_t range = (uint32_t)(P.Sq - q) * 4;
-      const i32x4 rl = make_rsrc(a.lse + hoff + q, range);
-      const i32x4 rdl = make_rsrc(a.delta + hoff + q, range);
-      dma16(rl, lane * 16, lds + 4 * TILE + buf * STAT);
-      dma16(rdl, lane * 16, lds + 4 * TILE + (2 + buf) * STAT);
-    }
+    TileCopy c;
+    c.rq = TileDma<D, BQ, NW>::rsrc(static_cast<const char*>(a.q) + hoff * RB, qb, P.Sq);
+    c.rdo = TileDma<D, BQ, NW>::rsrc(static_cast<const char*>(a.dout) + hoff * RB, qb, P.Sq);
+    const int q = qb < P.Sq ? qb : P.Sq;
+    c.rst = make_rsrc(((w & 1) ? a.delta : a.lse) + hoff + q, (uint32_t)(P.Sq - q) * 4);
+    c.buf = buf;
+    return c;
+  };
+  auto copy_part = [&](const TileCopy& c, int k) {
+    constexpr int IPW = TileDma<D, BQ, NW>::IPW;
+    if (k < IPW) dma.one(c.rq, k, lds + c.buf * TILE, w);
+    else if (k < 2 * IPW) dma.one(c.rdo, k - IPW, lds + (2 + c.buf) * TILE, w);
+    else dma16(c.rst, lane * 16, lds + 4 * TILE + (2 * (w & 1) + c.buf) * STAT);
+  };
+  auto issue = [&](int hq, int qb, int buf) {
+    const TileCopy c = plan(hq, qb, buf);
+#pragma unroll
+    for (int k = 0; k < NDMA; ++k) copy_part(c, k);
   };
 
   f32x16 dka[DT], dva[DT];
@@ -496,11 +524,13 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   // ahead (across phase boundaries; row fragments in A, transposed ones in C)
   // and the LSE / Delta of the E quad due next.  sched_barrier fences keep
   // the compiler to this order.
-  auto tile_fast = [&](const char* ql, const char* dl_, const float* lsel, const float* dltl) {
+  auto tile_fast = [&](const char* ql, const char* dl_, const float* lsel, const float* dltl, auto&& copy_k) {
     constexpr int KS = KSTEPS, NSTEP = 4 * KS, PF = APF, R = PF + 1;
     static_assert(2 * DT == KS && NQS == 2, "fast path shape");
-    // step of phase 1 / 2 at which E quad q is computed
-    auto quad_step = [](int q) { int s = (q + 1) * KS / 4 - 1; return s < 0 ? 0 : s; };
+    // E work in pairs of elements, spread evenly over the KS steps of its
+    // phase (phase 1 for sub-tile 0, phase 2 for sub-tile 1): pair p at step
+    // p * KS / 8, the LSE / Delta quad it needs read one step earlier.
+    auto pair_step = [](int p) { return p * KS / 8; };
     f32x16 sacc[2], pacc[2];
     zero(sacc[0]); zero(pacc[0]); zero(sacc[1]); zero(pacc[1]);
     frag pf[2][2], sf[2][2];
@@ -522,16 +552,16 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
       ls[j][q] = *reinterpret_cast<const f32x4*>(lsel + r0);
       dd[j][q] = *reinterpret_cast<const f32x4*>(dltl + r0);
     };
-    auto equad = [&](int j, int q) {
+    auto epair = [&](int j, int p) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int e = 4 * q + i;
-        const float pv = fast_exp2(fmaf(sacc[j][e], P.scale_log2, -ls[j][q][i] * kLog2e));
+      for (int i = 0; i < 2; ++i) {
+        const int e = 2 * p + i, q = e >> 2;
+        const float pv = fast_exp2(fmaf(sacc[j][e], P.scale_log2, -ls[j][q][e & 3] * kLog2e));
         sacc[j][e] = pv;
-        pacc[j][e] = pv * (pacc[j][e] - dd[j][q][i]);
+        pacc[j][e] = pv * (pacc[j][e] - dd[j][q][e & 3]);
       }
-      if (q & 1) {
-        const int half = q >> 1;
+      if ((p & 3) == 3) {
+        const int half = p >> 2;
         float x[8], y[8];
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
@@ -548,12 +578,12 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
     for (int t = 0; t < NSTEP; ++t) {
       const int ph = t / KS, s = t % KS;
       if (t + PF < NSTEP) load(t + PF);
-      // stats of the E quads computed in the next step
+      // stats of the quads whose first pair comes in the next step
 #pragma unroll
       for (int q = 0; q < 4; ++q)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-          if ((j + 1) * KS + quad_step(q) == t + 1) load_stats(j, q);
+          if ((j + 1) * KS + pair_step(2 * q) == t + 1) load_stats(j, q);
       if (ph < 2) {
         sacc[ph] = E::mma(ring[t % R][0], kf[s], sacc[ph]);
         pacc[ph] = E::mma(ring[t % R][1], vf[s], pacc[ph]);
@@ -564,9 +594,11 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
       }
       if (ph == 1 || ph == 2) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (quad_step(q) == s) equad(ph - 1, q);
+        for (int p = 0; p < 8; ++p)
+          if (pair_step(p) == s) epair(ph - 1, p);
       }
+      // the next tile's copies, one per step
+      if (t < NDMA) copy_k(t);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -592,19 +624,36 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   auto step = [&](int it, auto masked_c) {
     const int buf = it & 1;
     const int hq = hq_next, qbase = qb_next;
+    // past the last tile the copies target qb = Sq (zeros into the idle buffer)
     if (it + 1 < n_it) {
       hq_next = ref_next.hq;
       qb_next = walk.qbase(ref_next);
-      issue(hq_next, qb_next, buf ^ 1);
+    } else {
+      qb_next = P.Sq;
     }
-    if (it + 2 < n_it) ref_next = walk.fetch(it + 2);
-    if (qbase < P.Sq) {
-      const float* lsel = reinterpret_cast<const float*>(lds + 4 * TILE + buf * STAT);
-      const float* dltl = reinterpret_cast<const float*>(lds + 4 * TILE + (2 + buf) * STAT);
-      if constexpr (!decltype(masked_c)::value && !kMods && FA_DKDV_FAST)
-        tile_fast(lds + buf * TILE, lds + (2 + buf) * TILE, lsel, dltl);
-      else
+    const TileCopy next = plan(hq_next, qb_next, buf ^ 1);
+    auto copy_k = [&](int k) { copy_part(next, k); };
+    auto fetch_next = [&]() { ref_next = walk.fetch(min(it + 2, n_it - 1)); };
+    if constexpr (!decltype(masked_c)::value && !kMods && FA_DKDV_FAST) {
+      if (qbase < P.Sq) {
+        tile_fast(lds + buf * TILE, lds + (2 + buf) * TILE,
+                  reinterpret_cast<const float*>(lds + 4 * TILE + buf * STAT),
+                  reinterpret_cast<const float*>(lds + 4 * TILE + (2 + buf) * STAT), copy_k);
+        fetch_next();
+      } else {
+#pragma unroll
+        for (int k = 0; k < NDMA; ++k) copy_k(k);
+        fetch_next();
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < NDMA; ++k) copy_k(k);
+      fetch_next();
+      if (qbase < P.Sq) {
+        const float* lsel = reinterpret_cast<const float*>(lds + 4 * TILE + buf * STAT);
+        const float* dltl = reinterpret_cast<const float*>(lds + 4 * TILE + (2 + buf) * STAT);
         tile(hq, qbase, lds + buf * TILE, lds + (2 + buf) * TILE, lsel, dltl, masked_c);
+      }
     }
     wait_vmem();
     __syncthreads();

@@ -49,7 +49,7 @@ void fwd_bf16_kernel(FwdArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[4 * TILE];  // K0 K1 V0 V1
 
   const Problem& P = a.p;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 31, hh = lane >> 5;
   const int nqt = (P.Sq + BM - 1) / BM;
   int head, qt;
