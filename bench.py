@@ -152,6 +152,10 @@ def main():
     ap.add_argument("--config", default="c2")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--profile-kernel", choices=("fwd", "dkdv", "dq", "copy"), default=None,
+                    help="run only this kernel --profile-iters times and exit (for rocprofv3 counter passes; "
+                         "copy = a 256 MiB device copy used to calibrate FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--profile-iters", type=int, default=3)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported (run with --gpus 1)",
@@ -161,6 +165,15 @@ def main():
     import torch
     import pallas_flexattn as pf
     from pallas_flexattn.flash_attn import Runner
+
+    if args.profile_kernel == "copy":
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(args.profile_iters):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"profile: {args.profile_iters} copies of 256 MiB")
+        return
 
     cfg = make_config(args.config)
     B, Hq, Hkv, S, D = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["S"], cfg["D"]
@@ -176,6 +189,16 @@ def main():
     flop_fwd = 4.0 * D * pairs * Hq
     flop_bwd = 10.0 * D * pairs * Hq
     stream = torch.cuda.current_stream()
+
+    if args.profile_kernel:
+        runner.fwd()
+        runner.preprocess()
+        fn = {"fwd": runner.fwd, "dkdv": runner.dkdv, "dq": runner.dq_}[args.profile_kernel]
+        for _ in range(args.profile_iters):
+            fn()
+        torch.cuda.synchronize()
+        log(f"profile: {args.profile_kernel} x {args.profile_iters} on {args.config}")
+        return
 
     for _ in range(args.warmup):
         runner.step()
