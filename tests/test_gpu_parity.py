@@ -41,6 +41,13 @@ CASES = [
     ("dense-fp32-d32", "fp32", 1, 2, 2, 128, 32, ("none",), {}),
     ("causal-bf16-d32", "bf16", 1, 2, 2, 256, 32, ("causal",), {}),
     ("softcap-fp32-d128", "fp32", 1, 2, 1, 160, 128, ("causal",), {"softcap": 20.0, "alibi": True}),
+    # full tiles of several q heads walked before the partial ones (GQA group of 4, no score mods)
+    ("gqa-causal-bf16-d128", "bf16", 2, 8, 2, 384, 128, ("causal",), {}),
+    # a window wide enough for fully-live tiles inside it
+    ("window-wide-bf16-d128", "bf16", 1, 2, 2, 1024, 128, ("window", 300, 0), {}),
+    # mask blocks of 2 and 3 kernel tiles per side (power-of-two and general sub-tile walks)
+    ("causal-bf16-block256", "bf16", 1, 2, 2, 768, 128, ("causal",), {"block": 256}),
+    ("causal-bf16-block384-d64", "bf16", 1, 2, 2, 768, 64, ("causal",), {"block": 384}),
 ]
 
 
@@ -77,7 +84,7 @@ def test_flex_attention_fwd_bwd(case):
         if softcap:
             parts.append(pf.softcap_score_mod(softcap))
         score = pf.compose_score_mods(*parts)
-    bm = pf.create_block_mask(mm, B, Hq, S, S, 128) if mm is not None else None
+    bm = pf.create_block_mask(mm, B, Hq, S, S, extras.get("block", 128)) if mm is not None else None
 
     tq, tk, tv = (to_torch(x, dtype).requires_grad_() for x in (q, k, v))
     tdo = to_torch(do, dtype)
