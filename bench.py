@@ -156,6 +156,9 @@ def main():
                     help="run only this kernel --profile-iters times and exit (for rocprofv3 counter passes; "
                          "copy = a 256 MiB device copy used to calibrate FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--profile-iters", type=int, default=3)
+    ap.add_argument("--dense-ref", action="store_true",
+                    help="also time the same shape with no mask (every tile live) and report the time fraction "
+                         "next to the live-block fraction (sparse-proportionality check)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported (run with --gpus 1)",
@@ -226,6 +229,19 @@ def main():
     fwdbwd_tflops = (flop_fwd + flop_bwd) / (ms_step * 1e-3) / 1e12
     fwd_tflops = flop_fwd / (ms_fwd * 1e-3) / 1e12
 
+    sparsity = None
+    if args.dense_ref:
+        dense = Runner(tq, tk, tv, tdo, score_mod=cfg["score"])
+        for _ in range(args.warmup):
+            dense.step()
+        torch.cuda.synchronize()
+        dense_ms = time_region(dense.step, args.steps, stream)
+        del dense
+        live = 1.0 - bmask.sparsity
+        sparsity = {"live_block_fraction": round(live, 4), "dense_ms_per_step": round(dense_ms, 4),
+                    "time_fraction": round(ms_step / dense_ms, 4)}
+        log(f"dense reference {dense_ms:.3f} ms/step; time fraction {ms_step / dense_ms:.3f} vs live blocks {live:.3f}")
+
     cpu = None
     if not args.no_cpu:
         log("cpu baseline ...")
@@ -257,6 +273,8 @@ def main():
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic},
         "cpu_baseline": cpu,
     }
+    if sparsity is not None:
+        out["sparsity_check"] = sparsity
     print(json.dumps(out), flush=True)
 
 
