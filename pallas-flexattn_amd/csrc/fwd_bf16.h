@@ -28,6 +28,10 @@
 #include "dma.h"
 #include "fwd.h"
 
+#ifndef FA_FWD_OREG
+#define FA_FWD_OREG 'v'
+#endif
+
 namespace fa {
 
 template <int D, int BN, int NW, bool kMods>
@@ -145,6 +149,8 @@ void fwd_bf16_kernel(FwdArgs a) {
   for (int i = 0; i < DT; ++i)
 #pragma unroll
     for (int e = 0; e < 16; ++e) oacc[i][e] = 0.f;
+#pragma unroll
+  for (int i = 0; i < DT; ++i) mfma_drain<FA_FWD_OREG>(oacc[i]);
   // Reference maximum m (log2 units, per row) and partial sum l.  m may trail
   // the running maximum by up to kSlack: P = exp2(t - m) then stays below
   // 2^kSlack, and O, l are rescaled only when a row maximum outgrows it (the
@@ -168,9 +174,13 @@ void fwd_bf16_kernel(FwdArgs a) {
       const float alpha = fast_exp2(m - (mnew == -INFINITY ? 0.f : mnew));
       l *= alpha;
 #pragma unroll
+      for (int i = 0; i < DT; ++i) mfma_drain<FA_FWD_OREG>(oacc[i]);
+#pragma unroll
       for (int i = 0; i < DT; ++i)
 #pragma unroll
         for (int e = 0; e < 16; ++e) oacc[i][e] *= alpha;
+#pragma unroll
+      for (int i = 0; i < DT; ++i) mfma_drain<FA_FWD_OREG>(oacc[i]);
       m = mnew;
     }
     const float muse = m == -INFINITY ? 0.f : m;
@@ -268,13 +278,15 @@ void fwd_bf16_kernel(FwdArgs a) {
           const uint2 lo = lds_read_tr16(vl + voffT[i] + (16 * c) * RB);
           const uint2 hi = lds_read_tr16(vl + voffT[i] + (16 * c + 4) * RB);
           const frag vf = u32x4{lo.x, lo.y, hi.x, hi.y};
-          oacc[i] = E::mma(vf, pf[c], oacc[i]);
+          mfma_acc<FA_FWD_OREG>(oacc[i], vf, pf[c]);
         }
     }
     wait_vmem();
     __syncthreads();
   }
 
+#pragma unroll
+  for (int i = 0; i < DT; ++i) mfma_drain<FA_FWD_OREG>(oacc[i]);
   const float lt = pair_sum(l);
   const float inv = lt > 0.f ? 1.0f / lt : 0.f;
   if (qvalid) {
