@@ -28,6 +28,9 @@
 #include "dma.h"
 #include "fwd.h"
 
+#ifndef FA_FWD_PRIO
+#define FA_FWD_PRIO 1
+#endif
 #ifndef FA_FWD_OREG
 #define FA_FWD_OREG 'v'
 #endif
@@ -232,6 +235,7 @@ void fwd_bf16_kernel(FwdArgs a) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) sacc[j][e] = 0.f;
       frag ka[2][NSUB];
+      if (FA_FWD_PRIO) __builtin_amdgcn_s_setprio(1);  // MFMA phase first in issue order
 #pragma unroll
       for (int j = 0; j < NSUB; ++j) ka[0][j] = *reinterpret_cast<const u32x4*>(kl + j * 32 * RB + koffA[0]);
 #pragma unroll
@@ -244,6 +248,7 @@ void fwd_bf16_kernel(FwdArgs a) {
 #pragma unroll
         for (int j = 0; j < NSUB; ++j) sacc[j] = E::mma(ka[s & 1][j], qf[s], sacc[j]);
       }
+      if (FA_FWD_PRIO) __builtin_amdgcn_s_setprio(0);
 
       if constexpr (kMods) {
 #pragma unroll
@@ -271,6 +276,7 @@ void fwd_bf16_kernel(FwdArgs a) {
         for (int t = 0; t < 8; ++t) x[t] = sacc[c >> 1][8 * (c & 1) + t];
         pf[c] = E::pack(x);
       }
+      if (FA_FWD_PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int i = 0; i < DT; ++i)
 #pragma unroll
@@ -280,6 +286,7 @@ void fwd_bf16_kernel(FwdArgs a) {
           const frag vf = u32x4{lo.x, lo.y, hi.x, hi.y};
           mfma_acc<FA_FWD_OREG>(oacc[i], vf, pf[c]);
         }
+      if (FA_FWD_PRIO) __builtin_amdgcn_s_setprio(0);
     }
     wait_vmem();
     __syncthreads();
