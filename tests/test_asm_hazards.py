@@ -1,0 +1,104 @@
+"""Wait states after the inline-asm MFMAs of the gfx950 kernels (CPU: compiles to assembly).
+
+Accumulators that only MFMAs touch (dQ, dK, dV, O) are accumulated in place through inline asm
+(`mfma_acc` in csrc/common.h, the accumulator tied to the output), which the compiler's hazard
+recognizer cannot see into.  The ISA requires an MFMA's passes plus a few wait states before
+another unit reads (or overwrites) its destination registers; the kernels meet that with
+`mfma_drain` (20 wait states) before their own reads.  If register allocation ever copies or
+reads such an accumulator with a compiler-emitted instruction sooner, that instruction sees a
+stale value and the result is wrong only now and then, under load.  This test compiles the
+library to gfx950 assembly with the build flags and checks that every compiler-emitted
+instruction touching the destination of an inline-asm MFMA comes at least 20 wait states after
+it (`s_nop N` counts N + 1, any other instruction 1), scanning each kernel in fall-through
+order.  The scan is checked on a planted case: a copy two instructions after the MFMA."""
+import os
+import re
+import shutil
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+NEED = 20
+
+
+def _regs(tok):
+    m = re.match(r"([va])\[(\d+):(\d+)\]", tok)
+    if m:
+        return {(m.group(1), r) for r in range(int(m.group(2)), int(m.group(3)) + 1)}
+    m = re.match(r"([va])(\d+)$", tok)
+    return {(m.group(1), int(m.group(2)))} if m else set()
+
+
+def early_touches(asm_text):
+    """(kernel, line, wait states, instruction) for compiler-emitted instructions that touch an
+    inline-asm MFMA's destination registers fewer than NEED wait states after it."""
+    found = []
+    kern, inasm, pending = None, False, []  # pending: [dest regs, wait states since]
+    for i, line in enumerate(asm_text.split("\n")):
+        t = line.strip()
+        m = re.match(r"^(_Z\w+):", t)
+        if m:
+            kern, pending = m.group(1), []
+            continue
+        if t.startswith(";;#ASMSTART"):
+            inasm = True
+            continue
+        if t.startswith(";;#ASMEND"):
+            inasm = False
+            continue
+        if not t or t.startswith((".", ";")) or t.endswith(":"):
+            continue
+        op = t.split()[0]
+        ws = int(t.split()[1].rstrip(",")) + 1 if op == "s_nop" else 1
+        operands = [o.strip() for o in t[len(op):].split(";")[0].split(",")]
+        if inasm:
+            if op.startswith("v_mfma"):
+                pending.append([_regs(operands[0]), 0])
+        else:
+            used = set()
+            for o in operands:
+                if o:
+                    used |= _regs(o.split()[0])
+            for dest, since in pending:
+                if dest & used:
+                    found.append((kern, i + 1, since, t))
+        for p in pending:
+            p[1] += ws
+        pending = [p for p in pending if p[1] < NEED]
+    return found
+
+
+def test_scan_finds_planted_copy():
+    asm = "\n".join([
+        "_Zkernel:",
+        "\t;;#ASMSTART",
+        "\ts_nop 1",
+        "\tv_mfma_f32_32x32x16_bf16 v[2:17], v[20:23], v[24:27], v[2:17]",
+        "\t;;#ASMEND",
+        "\tv_add_f32_e32 v30, v31, v32",
+        "\tv_mov_b64_e32 v[40:41], v[16:17]",
+    ])
+    found = early_touches(asm)
+    assert [(f[0], f[2]) for f in found] == [("_Zkernel", 2)]
+    # after a drain the same copy is clean
+    drained = asm.replace("\tv_add_f32_e32", "\t;;#ASMSTART\n\ts_nop 7\n\ts_nop 7\n\ts_nop 3\n\t;;#ASMEND\n"
+                                               "\tv_add_f32_e32")
+    assert early_touches(drained) == []
+
+
+@pytest.mark.skipif(shutil.which("hipcc") is None and not os.path.exists("/opt/rocm/bin/hipcc"),
+                    reason="hipcc not available")
+def test_no_early_reads_of_asm_mfma_results(tmp_path):
+    sys.path.insert(0, os.path.join(ROOT, "pallas-flexattn_amd"))
+    import build as b
+    flags = [f for f in b.FLAGS if f not in ("-shared", "-fPIC")]
+    out = tmp_path / "capi.s"
+    res = subprocess.run([b.HIPCC, *flags, "--cuda-device-only", "-S", *b.SOURCES, "-o", str(out)],
+                         capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr[-2000:]
+    text = out.read_text()
+    assert ";;#ASMSTART" in text and "v_mfma" in text
+    found = early_touches(text)
+    assert not found, "\n".join(f"{k} line {ln}: {ws} wait states: {ins}" for k, ln, ws, ins in found[:20])
