@@ -371,6 +371,11 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
       vf[s] = buf_load16(rv, kw * RB + (2 * s + hh) * 16);
     }
   }
+  // V is kept negated (bf16 sign flips), so the dP MFMA accumulates -dP onto
+  // whatever its accumulator starts from: the fast path starts it from Delta
+  // and gets Delta - dP, dS = -P (Delta - dP) with one multiply per element.
+#pragma unroll
+  for (int s = 0; s < KSTEPS; ++s) vf[s] ^= 0x80008000u;
   int qlo, qhi;  // queries that see this lane's key (masks are intervals here)
   query_interval(P, b, kw, &qlo, &qhi);
 
@@ -478,8 +483,9 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
           if constexpr (kMods) pv = fast_exp2(sacc[e] - ls[i] * kLog2e);
           else pv = fast_exp2(fmaf(sacc[e], P.scale_log2, -ls[i] * kLog2e));
           sacc[e] = pv;
-          if constexpr (kMods) pacc[e] = pv * (pacc[e] - dt4[i]) * dsdx[e];
-          else pacc[e] = pv * (pacc[e] - dt4[i]);
+          // pacc = -dP (V negated): dS = P (dP - Delta) = -P (pacc + Delta)
+          if constexpr (kMods) pacc[e] = -pv * (pacc[e] + dt4[i]) * dsdx[e];
+          else pacc[e] = -pv * (pacc[e] + dt4[i]);
         }
       }
       frag pf[2], sf[2];
@@ -529,13 +535,23 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
     static_assert(2 * DT == KS && NQS == 2, "fast path shape");
     // E work in pairs of elements, spread evenly over the KS steps of its
     // phase (phase 1 for sub-tile 0, phase 2 for sub-tile 1): pair p at step
-    // p * KS / 8, the LSE / Delta quad it needs read one step earlier.
+    // p * KS / 8, the LSE quad it needs read one step earlier.
     auto pair_step = [](int p) { return p * KS / 8; };
     f32x16 sacc[2], pacc[2];
-    zero(sacc[0]); zero(pacc[0]); zero(sacc[1]); zero(pacc[1]);
+    zero(sacc[0]);
+    zero(sacc[1]);
+    // dP accumulates onto Delta: pacc = Delta - dP (V negated)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(dltl + 32 * j + acc_row(4 * q, hh));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pacc[j][4 * q + i] = d4[i];
+      }
     frag pf[2][2], sf[2][2];
     frag ring[R][2];
-    f32x4 ls[2][4], dd[2][4];
+    f32x4 ls[2][4];
     auto load = [&](int t) {
       const int ph = t / KS, s = t % KS;
       if (ph < 2) {
@@ -550,15 +566,24 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
     auto load_stats = [&](int j, int q) {
       const int r0 = 32 * j + acc_row(4 * q, hh);
       ls[j][q] = *reinterpret_cast<const f32x4*>(lsel + r0);
-      dd[j][q] = *reinterpret_cast<const f32x4*>(dltl + r0);
     };
-    auto epair = [&](int j, int p) {
+    // A pair's E work in two stages a step apart, so the exponentials'
+    // latency passes under the next step's MFMAs: e_exp (P), then e_use (dS,
+    // and the bf16 packing once a half of the sub-tile is complete).
+    float pvq[8][2];
+    auto e_exp = [&](int j, int p) {
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int e = 2 * p + i, q = e >> 2;
-        const float pv = fast_exp2(fmaf(sacc[j][e], P.scale_log2, -ls[j][q][e & 3] * kLog2e));
-        sacc[j][e] = pv;
-        pacc[j][e] = pv * (pacc[j][e] - dd[j][q][e & 3]);
+        pvq[p][i] = fast_exp2(fmaf(sacc[j][e], P.scale_log2, -ls[j][q][e & 3] * kLog2e));
+      }
+    };
+    auto e_use = [&](int j, int p) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int e = 2 * p + i;
+        sacc[j][e] = pvq[p][i];
+        pacc[j][e] = -pvq[p][i] * pacc[j][e];
       }
       if ((p & 3) == 3) {
         const int half = p >> 2;
@@ -578,7 +603,7 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
     for (int t = 0; t < NSTEP; ++t) {
       const int ph = t / KS, s = t % KS;
       if (t + PF < NSTEP) load(t + PF);
-      // stats of the quads whose first pair comes in the next step
+      // LSE of the quads whose first pair comes in the next step
 #pragma unroll
       for (int q = 0; q < 4; ++q)
 #pragma unroll
@@ -592,10 +617,15 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
         mfma_acc<'a'>(dva[s >> 1], ring[t % R][0], pf[j][s & 1]);
         mfma_acc<'a'>(dka[s >> 1], ring[t % R][1], sf[j][s & 1]);
       }
+      if (t > 0 && ((t - 1) / KS == 1 || (t - 1) / KS == 2)) {  // second stage of last step's pairs
+#pragma unroll
+        for (int p = 0; p < 8; ++p)
+          if (pair_step(p) == (t - 1) % KS) e_use((t - 1) / KS - 1, p);
+      }
       if (ph == 1 || ph == 2) {
 #pragma unroll
         for (int p = 0; p < 8; ++p)
-          if (pair_step(p) == s) epair(ph - 1, p);
+          if (pair_step(p) == s) e_exp(ph - 1, p);
       }
       // the next tile's copies, one per step
       if (t < NDMA) copy_k(t);
