@@ -10,7 +10,8 @@ stale value and the result is wrong only now and then, under load.  This test co
 library to gfx950 assembly with the build flags and checks that every compiler-emitted
 instruction touching the destination of an inline-asm MFMA comes at least 20 wait states after
 it (`s_nop N` counts N + 1, any other instruction 1), scanning each kernel in fall-through
-order.  The scan is checked on a planted case: a copy two instructions after the MFMA."""
+order.  The same assembly must name M0 only inside inline asm: the LDS-DMA asm sets M0 without
+restoring it.  Both scans are checked on planted cases."""
 import os
 import re
 import shutil
@@ -102,3 +103,26 @@ def test_no_early_reads_of_asm_mfma_results(tmp_path):
     assert ";;#ASMSTART" in text and "v_mfma" in text
     found = early_touches(text)
     assert not found, "\n".join(f"{k} line {ln}: {ws} wait states: {ins}" for k, ln, ws, ins in found[:20])
+    # The LDS-DMA asm (csrc/dma.h) sets M0 without restoring it, which is only sound while the
+    # compiler itself keeps nothing in M0.
+    m0 = m0_uses(text)
+    assert not m0, "compiler-emitted M0 uses: " + "; ".join(m0[:10])
+
+
+def m0_uses(asm_text):
+    """Compiler-emitted (outside inline asm) instructions that name M0."""
+    out, inasm = [], False
+    for line in asm_text.split("\n"):
+        t = line.strip()
+        if t.startswith(";;#ASMSTART"):
+            inasm = True
+        elif t.startswith(";;#ASMEND"):
+            inasm = False
+        elif not inasm and t and not t.startswith((";", ".")) and re.search(r"\bm0\b", t.split(";")[0]):
+            out.append(t)
+    return out
+
+
+def test_m0_scan_finds_planted_use():
+    asm = "\t;;#ASMSTART\n\ts_mov_b32 m0, s4\n\t;;#ASMEND\n\ts_mov_b32 m0, -1\n\tds_write_b32 v1, v2\n"
+    assert m0_uses(asm) == ["s_mov_b32 m0, -1"]
