@@ -402,33 +402,45 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   // over its MFMA steps (the texture unit takes one copy instruction at a
   // time; four waves issuing all of theirs at once after a barrier queue for
   // hundreds of cycles).  A tile at qb >= Sq copies zeros.
-  // Waves with even index copy the LSE tile, odd ones Delta (each wave one
-  // instruction, no branch; the duplicate writes carry identical data).
+  // Every wave copies the Delta tile by DMA and loads the LSE tile into a
+  // register (one value per lane), storing -LSE * log2(e) to LDS later in the
+  // step (stat_store), so the exponent needs one FMA per element instead of a
+  // multiply and an FMA.  The four waves' writes carry identical data; doing
+  // the same work in every wave keeps the fast path free of branches.
   struct TileCopy {
-    i32x4 rq, rdo, rst;
+    i32x4 rq, rdo, rdl, rls;
     int buf;
   };
-  constexpr int NDMA = 2 * TileDma<D, BQ, NW>::IPW + 1;
+  constexpr int NDMA = 2 * TileDma<D, BQ, NW>::IPW + 2;
   auto plan = [&](int hq, int qb, int buf) {
     const size_t hoff = (size_t)(b * P.Hq + hq) * P.Sq;
     TileCopy c;
     c.rq = TileDma<D, BQ, NW>::rsrc(static_cast<const char*>(a.q) + hoff * RB, qb, P.Sq);
     c.rdo = TileDma<D, BQ, NW>::rsrc(static_cast<const char*>(a.dout) + hoff * RB, qb, P.Sq);
     const int q = qb < P.Sq ? qb : P.Sq;
-    c.rst = make_rsrc(((w & 1) ? a.delta : a.lse) + hoff + q, (uint32_t)(P.Sq - q) * 4);
+    c.rdl = make_rsrc(a.delta + hoff + q, (uint32_t)(P.Sq - q) * 4);
+    c.rls = make_rsrc(a.lse + hoff + q, (uint32_t)(P.Sq - q) * 4);
     c.buf = buf;
     return c;
   };
+  static_assert(BQ <= 64, "one LSE value per lane");
+  float lse_in = 0.f;
   auto copy_part = [&](const TileCopy& c, int k) {
     constexpr int IPW = TileDma<D, BQ, NW>::IPW;
     if (k < IPW) dma.one(c.rq, k, lds + c.buf * TILE, w);
     else if (k < 2 * IPW) dma.one(c.rdo, k - IPW, lds + (2 + c.buf) * TILE, w);
-    else dma16(c.rst, lane * 16, lds + 4 * TILE + (2 * (w & 1) + c.buf) * STAT);
+    else if (k == 2 * IPW) dma16(c.rdl, lane * 16, lds + 4 * TILE + (2 + c.buf) * STAT);
+    else lse_in = __builtin_bit_cast(float, raw_buffer_load_b32(c.rls, lane * 4, 0, 0));
+  };
+  auto stat_store = [&](const TileCopy& c) {
+    // lanes past BQ store into the unused rest of the landing zone
+    *reinterpret_cast<float*>(lds + 4 * TILE + c.buf * STAT + lane * 4) = -lse_in * kLog2e;
   };
   auto issue = [&](int hq, int qb, int buf) {
     const TileCopy c = plan(hq, qb, buf);
 #pragma unroll
     for (int k = 0; k < NDMA; ++k) copy_part(c, k);
+    stat_store(c);
   };
 
   f32x16 dka[DT], dva[DT];
@@ -480,8 +492,8 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
         for (int i = 0; i < 4; ++i) {
           const int e = 4 * e4 + i;
           float pv;
-          if constexpr (kMods) pv = fast_exp2(sacc[e] - ls[i] * kLog2e);
-          else pv = fast_exp2(fmaf(sacc[e], P.scale_log2, -ls[i] * kLog2e));
+          if constexpr (kMods) pv = fast_exp2(sacc[e] + ls[i]);
+          else pv = fast_exp2(fmaf(sacc[e], P.scale_log2, ls[i]));
           sacc[e] = pv;
           // pacc = -dP (V negated): dS = P (dP - Delta) = -P (pacc + Delta)
           if constexpr (kMods) pacc[e] = -pv * (pacc[e] + dt4[i]) * dsdx[e];
@@ -530,7 +542,8 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   // ahead (across phase boundaries; row fragments in A, transposed ones in C)
   // and the LSE / Delta of the E quad due next.  sched_barrier fences keep
   // the compiler to this order.
-  auto tile_fast = [&](const char* ql, const char* dl_, const float* lsel, const float* dltl, auto&& copy_k) {
+  auto tile_fast = [&](const char* ql, const char* dl_, const float* lsel, const float* dltl, auto&& copy_k,
+                       auto&& stat_k) {
     constexpr int KS = KSTEPS, NSTEP = 4 * KS, PF = APF, R = PF + 1;
     static_assert(2 * DT == KS && NQS == 2, "fast path shape");
     // E work in pairs of elements, spread evenly over the KS steps of its
@@ -575,7 +588,7 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int e = 2 * p + i, q = e >> 2;
-        pvq[p][i] = fast_exp2(fmaf(sacc[j][e], P.scale_log2, -ls[j][q][e & 3] * kLog2e));
+        pvq[p][i] = fast_exp2(fmaf(sacc[j][e], P.scale_log2, ls[j][q][e & 3]));
       }
     };
     auto e_use = [&](int j, int p) {
@@ -627,8 +640,9 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
         for (int p = 0; p < 8; ++p)
           if (pair_step(p) == s) e_exp(ph - 1, p);
       }
-      // the next tile's copies, one per step
+      // the next tile's copies, one per step; its LSE stored near the end
       if (t < NDMA) copy_k(t);
+      if (t == NSTEP - 2) stat_k();
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -663,17 +677,19 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
     }
     const TileCopy next = plan(hq_next, qb_next, buf ^ 1);
     auto copy_k = [&](int k) { copy_part(next, k); };
+    auto stat_k = [&]() { stat_store(next); };
     auto fetch_next = [&]() { ref_next = walk.fetch(min(it + 2, n_it - 1)); };
     if constexpr (!decltype(masked_c)::value && !kMods && FA_DKDV_FAST) {
       if (qbase < P.Sq) {
         tile_fast(lds + buf * TILE, lds + (2 + buf) * TILE,
                   reinterpret_cast<const float*>(lds + 4 * TILE + buf * STAT),
-                  reinterpret_cast<const float*>(lds + 4 * TILE + (2 + buf) * STAT), copy_k);
+                  reinterpret_cast<const float*>(lds + 4 * TILE + (2 + buf) * STAT), copy_k, stat_k);
         fetch_next();
       } else {
 #pragma unroll
         for (int k = 0; k < NDMA; ++k) copy_k(k);
         fetch_next();
+        stat_k();
       }
     } else {
 #pragma unroll
@@ -684,6 +700,7 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
         const float* dltl = reinterpret_cast<const float*>(lds + 4 * TILE + (2 + buf) * STAT);
         tile(hq, qbase, lds + buf * TILE, lds + (2 + buf) * TILE, lsel, dltl, masked_c);
       }
+      stat_k();
     }
     wait_vmem();
     __syncthreads();
