@@ -402,39 +402,40 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   // over its MFMA steps (the texture unit takes one copy instruction at a
   // time; four waves issuing all of theirs at once after a barrier queue for
   // hundreds of cycles).  A tile at qb >= Sq copies zeros.
-  // Every wave copies the Delta tile by DMA and loads the LSE tile into a
-  // register (one value per lane), storing -LSE * log2(e) to LDS later in the
-  // step (stat_store), so the exponent needs one FMA per element instead of a
-  // multiply and an FMA.  The four waves' writes carry identical data; doing
-  // the same work in every wave keeps the fast path free of branches.
+  // The LSE and Delta tiles go through a register (one value per lane):
+  // waves 0, 1 load LSE and store -LSE * log2(e) later in the step
+  // (stat_store), so the exponent needs one FMA per element; waves 2, 3 load
+  // and store Delta.  The choice is a wave-uniform select, not a branch, and
+  // each pair of waves writes identical data.
   struct TileCopy {
-    i32x4 rq, rdo, rdl, rls;
+    i32x4 rq, rdo, rst;
     int buf;
   };
-  constexpr int NDMA = 2 * TileDma<D, BQ, NW>::IPW + 2;
+  constexpr int NDMA = 2 * TileDma<D, BQ, NW>::IPW + 1;
+  const bool stat_delta = (w & 2) != 0;
+  const float stat_scale = stat_delta ? 1.0f : -kLog2e;
   auto plan = [&](int hq, int qb, int buf) {
     const size_t hoff = (size_t)(b * P.Hq + hq) * P.Sq;
     TileCopy c;
     c.rq = TileDma<D, BQ, NW>::rsrc(static_cast<const char*>(a.q) + hoff * RB, qb, P.Sq);
     c.rdo = TileDma<D, BQ, NW>::rsrc(static_cast<const char*>(a.dout) + hoff * RB, qb, P.Sq);
     const int q = qb < P.Sq ? qb : P.Sq;
-    c.rdl = make_rsrc(a.delta + hoff + q, (uint32_t)(P.Sq - q) * 4);
-    c.rls = make_rsrc(a.lse + hoff + q, (uint32_t)(P.Sq - q) * 4);
+    c.rst = make_rsrc((stat_delta ? a.delta : a.lse) + hoff + q, (uint32_t)(P.Sq - q) * 4);
     c.buf = buf;
     return c;
   };
   static_assert(BQ <= 64, "one LSE value per lane");
-  float lse_in = 0.f;
+  float stat_in = 0.f;
   auto copy_part = [&](const TileCopy& c, int k) {
     constexpr int IPW = TileDma<D, BQ, NW>::IPW;
     if (k < IPW) dma.one(c.rq, k, lds + c.buf * TILE, w);
     else if (k < 2 * IPW) dma.one(c.rdo, k - IPW, lds + (2 + c.buf) * TILE, w);
-    else if (k == 2 * IPW) dma16(c.rdl, lane * 16, lds + 4 * TILE + (2 + c.buf) * STAT);
-    else lse_in = __builtin_bit_cast(float, raw_buffer_load_b32(c.rls, lane * 4, 0, 0));
+    else stat_in = __builtin_bit_cast(float, raw_buffer_load_b32(c.rst, lane * 4, 0, 0));
   };
   auto stat_store = [&](const TileCopy& c) {
     // lanes past BQ store into the unused rest of the landing zone
-    *reinterpret_cast<float*>(lds + 4 * TILE + c.buf * STAT + lane * 4) = -lse_in * kLog2e;
+    *reinterpret_cast<float*>(lds + 4 * TILE + ((stat_delta ? 2 : 0) + c.buf) * STAT + lane * 4) =
+        stat_in * stat_scale;
   };
   auto issue = [&](int hq, int qb, int buf) {
     const TileCopy c = plan(hq, qb, buf);
