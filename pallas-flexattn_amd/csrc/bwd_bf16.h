@@ -609,6 +609,9 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
         }
         pf[j][half] = E::pack(x);
         sf[j][half] = E::pack(y);
+        // the 2 wait states an MFMA needs after a VALU write of its operand
+        // (a half can be read in the very next step)
+        asm volatile("s_nop 1" : "+v"(pf[j][half]), "+v"(sf[j][half]));
       }
     };
 #pragma unroll
@@ -628,8 +631,9 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
         pacc[ph] = E::mma(ring[t % R][1], vf[s], pacc[ph]);
       } else {
         const int j = ph - 2;
-        mfma_acc<'a'>(dva[s >> 1], ring[t % R][0], pf[j][s & 1]);
-        mfma_acc<'a'>(dka[s >> 1], ring[t % R][1], sf[j][s & 1]);
+        // the packing fences P and dS (see e_use), so no s_nop here
+        mfma_acc<'a', false>(dva[s >> 1], ring[t % R][0], pf[j][s & 1]);
+        mfma_acc<'a', false>(dka[s >> 1], ring[t % R][1], sf[j][s & 1]);
       }
       if (t > 0 && ((t - 1) / KS == 1 || (t - 1) / KS == 2)) {  // second stage of last step's pairs
 #pragma unroll

@@ -113,16 +113,21 @@ constexpr int kSchedValu = 0x002;
 // the compiler's hazard recognizer, so the wait states the ISA requires are
 // explicit:
 //   * a VALU write of A or B needs 2 wait states before an MFMA reads it:
-//     every call starts with s_nop 1;
+//     every call starts with s_nop 1, unless kNop is false (for schedules
+//     whose operands are written at least a step before);
 //   * an MFMA result (8-pass XDL) needs up to 12 wait states before another
 //     unit reads it: mfma_drain() after the last accumulation;
 //   * back-to-back accumulation into the same registers needs none.
-template <char kReg>
+template <char kReg, bool kNop = true>
 __device__ __forceinline__ void mfma_acc(f32x16& acc, u32x4 a, u32x4 b) {
-  if constexpr (kReg == 'a')
+  if constexpr (kReg == 'a' && kNop)
     asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
-  else
+  else if constexpr (kReg == 'a')
+    asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+  else if constexpr (kNop)
     asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
+  else
+    asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
 }
 // Orders later reads of acc after 20 wait states (and earlier writes of acc,
 // e.g. zero-initialisation, before later MFMAs by at least as much).

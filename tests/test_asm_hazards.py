@@ -10,8 +10,10 @@ stale value and the result is wrong only now and then, under load.  This test co
 library to gfx950 assembly with the build flags and checks that every compiler-emitted
 instruction touching the destination of an inline-asm MFMA comes at least 20 wait states after
 it (`s_nop N` counts N + 1, any other instruction 1), scanning each kernel in fall-through
-order.  The same assembly must name M0 only inside inline asm: the LDS-DMA asm sets M0 without
-restoring it.  Both scans are checked on planted cases."""
+order.  In the other direction, an inline-asm MFMA must not read an A or B operand that a
+compiler-emitted VALU instruction wrote fewer than 2 wait states before (the schedules that drop
+`mfma_acc`'s leading `s_nop 1` rely on this).  The same assembly must name M0 only inside inline
+asm: the LDS-DMA asm sets M0 without restoring it.  Each scan is checked on a planted case."""
 import os
 import re
 import shutil
@@ -71,6 +73,54 @@ def early_touches(asm_text):
     return found
 
 
+def late_operands(asm_text):
+    """(kernel, line, wait states, instruction) for inline-asm MFMAs that read an A or B operand a
+    compiler-emitted VALU instruction wrote fewer than 2 wait states before (the asm's own s_nop
+    counts)."""
+    found = []
+    kern, inasm, recent = None, False, []  # recent: [regs written, wait states since]
+    for i, line in enumerate(asm_text.split("\n")):
+        t = line.strip()
+        m = re.match(r"^(_Z\w+):", t)
+        if m:
+            kern, recent = m.group(1), []
+            continue
+        if t.startswith(";;#ASMSTART"):
+            inasm = True
+            continue
+        if t.startswith(";;#ASMEND"):
+            inasm = False
+            continue
+        if not t or t.startswith((".", ";")) or t.endswith(":"):
+            continue
+        op = t.split()[0]
+        ws = int(t.split()[1].rstrip(",")) + 1 if op == "s_nop" else 1
+        operands = [o.strip() for o in t[len(op):].split(";")[0].split(",")]
+        if inasm and op.startswith("v_mfma"):
+            srcs = _regs(operands[1]) | _regs(operands[2])
+            for regs, since in recent:
+                if since < 2 and regs & srcs:
+                    found.append((kern, i + 1, since, t))
+        for r in recent:
+            r[1] += ws
+        recent = [r for r in recent if r[1] < 2]
+        if not inasm and op.startswith("v_") and not op.startswith("v_mfma") and operands[0]:
+            recent.append([_regs(operands[0].split()[0]), 0])
+    return found
+
+
+def test_scan_finds_planted_late_operand():
+    asm = "\n".join([
+        "_Zkernel:",
+        "\tv_cvt_pk_bf16_f32 v25, v1, v2",
+        "\t;;#ASMSTART",
+        "\tv_mfma_f32_32x32x16_bf16 a[0:15], v[20:23], v[24:27], a[0:15]",
+        "\t;;#ASMEND",
+    ])
+    assert [(f[0], f[2]) for f in late_operands(asm)] == [("_Zkernel", 0)]
+    assert late_operands(asm.replace("\t;;#ASMSTART\n", "\t;;#ASMSTART\n\ts_nop 1\n")) == []
+
+
 def test_scan_finds_planted_copy():
     asm = "\n".join([
         "_Zkernel:",
@@ -107,6 +157,8 @@ def test_no_early_reads_of_asm_mfma_results(tmp_path):
     # compiler itself keeps nothing in M0.
     m0 = m0_uses(text)
     assert not m0, "compiler-emitted M0 uses: " + "; ".join(m0[:10])
+    late = late_operands(text)
+    assert not late, "\n".join(f"{k} line {ln}: {ws} wait states: {ins}" for k, ln, ws, ins in late[:20])
 
 
 def m0_uses(asm_text):
