@@ -273,13 +273,15 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
         for (int t = 0; t < 8; ++t) y[t] = pacc[8 * half + t];
         sf[half] = E::pack(y);
       }
+      // the 2 wait states an MFMA needs after a VALU write of its operand
+      asm volatile("s_nop 1" : "+v"(sf[0]), "+v"(sf[1]));
       // x = (d tile, chunk half) of this sub-tile: chunk c = 2j + half
       frag kt[2];
       kt[0] = rt.t_frag(kl, 0, 2 * j);
 #pragma unroll
       for (int x = 0; x < 2 * DT; ++x) {
         if (x + 1 < 2 * DT) kt[(x + 1) & 1] = rt.t_frag(kl, (x + 1) >> 1, 2 * j + ((x + 1) & 1));
-        mfma_acc<'v'>(dqa[x >> 1], kt[x & 1], sf[x & 1]);
+        mfma_acc<'v', false>(dqa[x >> 1], kt[x & 1], sf[x & 1]);
       }
     }
   };

@@ -276,6 +276,13 @@ void fwd_bf16_kernel(FwdArgs a) {
         for (int t = 0; t < 8; ++t) x[t] = sacc[c >> 1][8 * (c & 1) + t];
         pf[c] = E::pack(x);
       }
+      // the 2 wait states an MFMA needs after a VALU write of its operand,
+      // once for all of P (the PV MFMAs then carry no s_nop)
+      static_assert(BN / 16 == 4 || BN / 16 == 2, "P fragments");
+      if constexpr (BN / 16 == 4)
+        asm volatile("s_nop 1" : "+v"(pf[0]), "+v"(pf[1]), "+v"(pf[2]), "+v"(pf[3]));
+      else
+        asm volatile("s_nop 1" : "+v"(pf[0]), "+v"(pf[1]));
       if (FA_FWD_PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int i = 0; i < DT; ++i)
@@ -284,7 +291,7 @@ void fwd_bf16_kernel(FwdArgs a) {
           const uint2 lo = lds_read_tr16(vl + voffT[i] + (16 * c) * RB);
           const uint2 hi = lds_read_tr16(vl + voffT[i] + (16 * c + 4) * RB);
           const frag vf = u32x4{lo.x, lo.y, hi.x, hi.y};
-          mfma_acc<FA_FWD_OREG>(oacc[i], vf, pf[c]);
+          mfma_acc<FA_FWD_OREG, false>(oacc[i], vf, pf[c]);
         }
       if (FA_FWD_PRIO) __builtin_amdgcn_s_setprio(0);
     }
