@@ -148,7 +148,9 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed warm-up steps (default: at least 3 steps and 0.5 s, so the GPU clock has "
+                         "settled before the timed steps; the count used is reported)")
     ap.add_argument("--config", default="c2")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -203,8 +205,17 @@ def main():
         log(f"profile: {args.profile_kernel} x {args.profile_iters} on {args.config}")
         return
 
-    for _ in range(args.warmup):
-        runner.step()
+    if args.warmup is None:
+        # the clock ramps up over the first tens of milliseconds of load
+        args.warmup, t_start = 0, time.perf_counter()
+        while args.warmup < 3 or time.perf_counter() - t_start < 0.5:
+            runner.step()
+            args.warmup += 1
+            if args.warmup % 8 == 0:
+                torch.cuda.synchronize()
+    else:
+        for _ in range(args.warmup):
+            runner.step()
     torch.cuda.synchronize()
     log(f"warmup done ({args.warmup} steps)")
     torch.cuda.synchronize()
