@@ -19,6 +19,10 @@ FLAGS = [
     # MFMA accumulators in VGPRs where they fit: fewer AGPR<->VGPR copies in
     # the backward kernels (about 3% faster there, forward unchanged)
     "-mllvm", "-amdgpu-mfma-vgpr-form=1",
+    # the hand-ordered tiles are fully unrolled step sequences; past the default
+    # size limit a partly unrolled loop indexes the register arrays dynamically
+    # and they go to scratch
+    "-mllvm", "-pragma-unroll-threshold=200000",
     "-I" + os.path.join(REPO, "include"),
 ]
 

@@ -545,10 +545,34 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   // ahead (across phase boundaries; row fragments in A, transposed ones in C)
   // and the LSE / Delta of the E quad due next.  sched_barrier fences keep
   // the compiler to this order.
-  auto tile_fast = [&](const char* ql, const char* dl_, const float* lsel, const float* dltl, auto&& copy_k,
-                       auto&& stat_k) {
+  auto tile_fast = [&](int qbase, const char* ql, const char* dl_, const float* lsel, const float* dltl,
+                       auto&& copy_k, auto&& stat_k, auto masked_c) {
+    constexpr bool kMasked = decltype(masked_c)::value;
     constexpr int KS = KSTEPS, NSTEP = 4 * KS, PF = APF, R = PF + 1;
     static_assert(2 * DT == KS && NQS == 2, "fast path shape");
+    // Partial tiles: element e of sub-tile j is query qbase + 32 j + 8 hh +
+    // r(e), r(e) = acc_row(e, 0) < 24.  rmask[j] has bit r set iff that query
+    // sees this lane's key; the packed P and dS words are ANDed with the
+    // matching 0 / 0xffff halves, so masked elements contribute exact zeros
+    // whatever their exponential came out as.
+    uint32_t rmask[2] = {0u, 0u};
+    if constexpr (kMasked) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int base = qbase + 32 * j + 8 * hh;
+        const int lo = max(qlo - base, 0), hi = min(qhi - base, 31);
+        const uint32_t up = 0xffffffffu >> (31 - max(hi, 0));
+        const uint32_t dn = 0xffffffffu << min(lo, 31);
+        rmask[j] = (hi >= lo) ? (up & dn) : 0u;
+      }
+    }
+    // 0xffff / 0 halves for the two elements of pair p (rows r, r + 1)
+    auto pair_mask = [&](int j, int p) {
+      const int r = acc_row(2 * p, 0);
+      const uint32_t lo = (uint32_t)__builtin_amdgcn_sbfe((int)rmask[j], r, 1);
+      const uint32_t hi = (uint32_t)__builtin_amdgcn_sbfe((int)rmask[j], r + 1, 1);
+      return (lo & 0xffffu) | (hi & 0xffff0000u);
+    };
     // E work in pairs of elements, spread evenly over the KS steps of its
     // phase (phase 1 for sub-tile 0, phase 2 for sub-tile 1): pair p at step
     // p * KS / 8, the LSE quad it needs read one step earlier.
@@ -611,6 +635,14 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
         }
         pf[j][half] = E::pack(x);
         sf[j][half] = E::pack(y);
+        if constexpr (kMasked) {
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const uint32_t m = pair_mask(j, 4 * half + w);
+            pf[j][half][w] &= m;
+            sf[j][half][w] &= m;
+          }
+        }
         // the 2 wait states an MFMA needs after a VALU write of its operand
         // (a half can be read in the very next step)
         asm volatile("s_nop 1" : "+v"(pf[j][half]), "+v"(sf[j][half]));
@@ -686,11 +718,11 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
     auto copy_k = [&](int k) { copy_part(next, k); };
     auto stat_k = [&]() { stat_store(next); };
     auto fetch_next = [&]() { ref_next = walk.fetch(min(it + 2, n_it - 1)); };
-    if constexpr (!decltype(masked_c)::value && !kMods && FA_DKDV_FAST) {
+    if constexpr (!kMods && FA_DKDV_FAST) {
       if (qbase < P.Sq) {
-        tile_fast(lds + buf * TILE, lds + (2 + buf) * TILE,
+        tile_fast(qbase, lds + buf * TILE, lds + (2 + buf) * TILE,
                   reinterpret_cast<const float*>(lds + 4 * TILE + buf * STAT),
-                  reinterpret_cast<const float*>(lds + 4 * TILE + (2 + buf) * STAT), copy_k, stat_k);
+                  reinterpret_cast<const float*>(lds + 4 * TILE + (2 + buf) * STAT), copy_k, stat_k, masked_c);
         fetch_next();
       } else {
 #pragma unroll
