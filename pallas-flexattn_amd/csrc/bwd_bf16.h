@@ -17,7 +17,8 @@
 //                    dQ^T += K^T dS^T over the kv-side block tables.
 //   dkdv_bf16_kernel (batch, kv head, 32*NW keys): K, V rows in VGPRs;
 //                    S = Q K^T, dP = dO V^T, dV^T += dO^T P, dK^T += Q^T dS
-//                    over the q-side tables of every q head of the GQA group.
+//                    over the q-side tables of every q head of the GQA group,
+//                    each q tile one hand-ordered step sequence.
 // Partial tiles apply the element mask, an interval per lane (windows and
 // contiguous documents; other document layouts use the generic kernels);
 // full tiles skip it.
@@ -27,14 +28,8 @@
 #include "bwd.h"
 #include "dma.h"
 
-#ifndef FA_DKDV_FAST
-#define FA_DKDV_FAST 1
-#endif
 #ifndef FA_DKDV_APF
 #define FA_DKDV_APF 2
-#endif
-#ifndef FA_DKDV_CPF
-#define FA_DKDV_CPF 2
 #endif
 
 namespace fa {
@@ -347,7 +342,7 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   constexpr int NC = BQ / 16;
   constexpr int TILE = BQ * RB;
   constexpr int STAT = 1024;  // LSE / Delta landing zone per buffer (BQ floats used)
-  constexpr int APF = FA_DKDV_APF, CPF = FA_DKDV_CPF;  // operand prefetch depths (steps)
+  constexpr int APF = FA_DKDV_APF;  // operand prefetch depth (steps)
   static_assert(BQ * 4 <= STAT, "stat tile");
   __shared__ __attribute__((aligned(1024))) char lds[4 * TILE + 4 * STAT];  // Q0 Q1 dO0 dO1 L0 L1 D0 D1
 
@@ -455,98 +450,19 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
     mfma_drain<'a'>(dva[i]);
   }
 
-  // One q tile, one code path for full and partial tiles (only the in-place
-  // masking of S is conditional).  Per 32-query sub-tile: S, dP -> P, dS
-  // (packed, rows = queries, column = this lane's key), then that sub-tile's
-  // share of dV^T += dO^T P and dK^T += Q^T dS (transposed fragments one step
-  // ahead), so the next sub-tile's MFMAs can overlap this one's exponentials.
-  auto tile = [&](int hq, int qbase, const char* ql, const char* dl_, const float* lsel, const float* dltl,
-                  auto masked_c) {
-    constexpr bool kMasked = decltype(masked_c)::value;
-    const float slope = P.alibi ? P.alibi[hq] : 0.f;
-#pragma unroll
-    for (int j = 0; j < NQS; ++j) {
-      f32x16 sacc, pacc;
-      zero(sacc);
-      zero(pacc);
-      mma_rows2<D, APF>(rt, ql, dl_, j, kf, vf, sacc, pacc);
-      float dsdx[16];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        dsdx[e] = 1.f;
-        if constexpr (kMods) {
-          const int qi = qbase + 32 * j + acc_row(e, hh);
-          sacc[e] = score_t<true>(P, sacc[e], slope, qi, kw, &dsdx[e]);
-        }
-      }
-      if constexpr (kMasked) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int qi = qbase + 32 * j + acc_row(e, hh);
-          sacc[e] = (qi >= qlo && qi <= qhi) ? sacc[e] : -INFINITY;
-        }
-      }
-#pragma unroll
-      for (int e4 = 0; e4 < 4; ++e4) {
-        const int r0 = 32 * j + acc_row(4 * e4, hh);
-        const f32x4 ls = *reinterpret_cast<const f32x4*>(lsel + r0);
-        const f32x4 dt4 = *reinterpret_cast<const f32x4*>(dltl + r0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int e = 4 * e4 + i;
-          float pv;
-          if constexpr (kMods) pv = fast_exp2(sacc[e] + ls[i]);
-          else pv = fast_exp2(fmaf(sacc[e], P.scale_log2, ls[i]));
-          sacc[e] = pv;
-          // pacc = -dP (V negated): dS = P (dP - Delta) = -P (pacc + Delta)
-          if constexpr (kMods) pacc[e] = -pv * (pacc[e] + dt4[i]) * dsdx[e];
-          else pacc[e] = -pv * (pacc[e] + dt4[i]);
-        }
-      }
-      frag pf[2], sf[2];
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        float x[8], y[8];
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          x[t] = sacc[8 * half + t];
-          y[t] = pacc[8 * half + t];
-        }
-        pf[half] = E::pack(x);
-        sf[half] = E::pack(y);
-      }
-      // x = (d tile, chunk half) of this sub-tile: chunk c = 2j + half;
-      // transposed fragments fetched CPF steps ahead
-      constexpr int CR = CPF + 1;
-      frag ft[CR][2];
-#pragma unroll
-      for (int x = 0; x < CPF; ++x) {
-        ft[x][0] = rt.t_frag(dl_, x >> 1, 2 * j + (x & 1));
-        ft[x][1] = rt.t_frag(ql, x >> 1, 2 * j + (x & 1));
-      }
-#pragma unroll
-      for (int x = 0; x < 2 * DT; ++x) {
-        if (x + CPF < 2 * DT) {
-          ft[(x + CPF) % CR][0] = rt.t_frag(dl_, (x + CPF) >> 1, 2 * j + ((x + CPF) & 1));
-          ft[(x + CPF) % CR][1] = rt.t_frag(ql, (x + CPF) >> 1, 2 * j + ((x + CPF) & 1));
-        }
-        mfma_acc<'a'>(dva[x >> 1], ft[x % CR][0], pf[x & 1]);
-        mfma_acc<'a'>(dka[x >> 1], ft[x % CR][1], sf[x & 1]);
-      }
-    }
-  };
-
-  // Full tiles without score mods: the q tile is a fixed sequence of 4*KS
-  // steps of two MFMAs each, in four phases
+  // One q tile (full or partial, with or without score mods): a fixed
+  // sequence of 4*KS steps of two MFMAs each, in four phases
   //   A0: S_0, dP_0  |  A1: S_1, dP_1  |  C0: dV^T, dK^T += (sub-tile 0)  |  C1
   // with the exponentials / dS of sub-tile 0 (E0) spread over A1's steps and
   // those of sub-tile 1 (E1) over C0's, so VALU work issues while the matrix
   // core is busy.  Every step also fetches the LDS operands of the step PF
   // ahead (across phase boundaries; row fragments in A, transposed ones in C)
-  // and the LSE / Delta of the E quad due next.  sched_barrier fences keep
+  // and the LSE quad due next (Delta is the dP MFMAs' initial value, read at
+  // the start).  Score mods, when present, are evaluated branch-free in the
+  // exponential's stage.  sched_barrier fences keep
   // the compiler to this order.
-  auto tile_fast = [&](int qbase, const char* ql, const char* dl_, const float* lsel, const float* dltl,
-                       auto&& copy_k, auto&& stat_k, auto masked_c) {
+  auto tile_fast = [&](int qbase, float slope, const char* ql, const char* dl_, const float* lsel,
+                       const float* dltl, auto&& copy_k, auto&& stat_k, auto masked_c) {
     constexpr bool kMasked = decltype(masked_c)::value;
     constexpr int KS = KSTEPS, NSTEP = 4 * KS, PF = APF, R = PF + 1;
     static_assert(2 * DT == KS && NQS == 2, "fast path shape");
@@ -610,12 +526,20 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
     // A pair's E work in two stages a step apart, so the exponentials'
     // latency passes under the next step's MFMAs: e_exp (P), then e_use (dS,
     // and the bf16 packing once a half of the sub-tile is complete).
-    float pvq[8][2];
+    float pvq[8][2], dsq[8][2];
+    const float cap_inv = P.softcap > 0.f ? 1.0f / P.softcap : 0.f;
     auto e_exp = [&](int j, int p) {
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int e = 2 * p + i, q = e >> 2;
-        pvq[p][i] = fast_exp2(fmaf(sacc[j][e], P.scale_log2, ls[j][q][e & 3]));
+        if constexpr (kMods) {
+          // score mods (log2-domain logit) and d s / d(scale q.k) for dS
+          const float t = score_mods_flat(sacc[j][e], P.scale, slope, qbase + 32 * j + acc_row(e, hh), kw,
+                                          P.softcap, cap_inv, &dsq[p][i]);
+          pvq[p][i] = fast_exp2(t + ls[j][q][e & 3]);
+        } else {
+          pvq[p][i] = fast_exp2(fmaf(sacc[j][e], P.scale_log2, ls[j][q][e & 3]));
+        }
       }
     };
     auto e_use = [&](int j, int p) {
@@ -623,7 +547,8 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
       for (int i = 0; i < 2; ++i) {
         const int e = 2 * p + i;
         sacc[j][e] = pvq[p][i];
-        pacc[j][e] = -pvq[p][i] * pacc[j][e];
+        if constexpr (kMods) pacc[j][e] = -pvq[p][i] * pacc[j][e] * dsq[p][i];
+        else pacc[j][e] = -pvq[p][i] * pacc[j][e];
       }
       if ((p & 3) == 3) {
         const int half = p >> 2;
@@ -718,27 +643,16 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
     auto copy_k = [&](int k) { copy_part(next, k); };
     auto stat_k = [&]() { stat_store(next); };
     auto fetch_next = [&]() { ref_next = walk.fetch(min(it + 2, n_it - 1)); };
-    if constexpr (!kMods && FA_DKDV_FAST) {
-      if (qbase < P.Sq) {
-        tile_fast(qbase, lds + buf * TILE, lds + (2 + buf) * TILE,
-                  reinterpret_cast<const float*>(lds + 4 * TILE + buf * STAT),
-                  reinterpret_cast<const float*>(lds + 4 * TILE + (2 + buf) * STAT), copy_k, stat_k, masked_c);
-        fetch_next();
-      } else {
-#pragma unroll
-        for (int k = 0; k < NDMA; ++k) copy_k(k);
-        fetch_next();
-        stat_k();
-      }
+    if (qbase < P.Sq) {
+      const float slope = (kMods && P.alibi) ? P.alibi[hq] : 0.f;
+      tile_fast(qbase, slope, lds + buf * TILE, lds + (2 + buf) * TILE,
+                reinterpret_cast<const float*>(lds + 4 * TILE + buf * STAT),
+                reinterpret_cast<const float*>(lds + 4 * TILE + (2 + buf) * STAT), copy_k, stat_k, masked_c);
+      fetch_next();
     } else {
 #pragma unroll
       for (int k = 0; k < NDMA; ++k) copy_k(k);
       fetch_next();
-      if (qbase < P.Sq) {
-        const float* lsel = reinterpret_cast<const float*>(lds + 4 * TILE + buf * STAT);
-        const float* dltl = reinterpret_cast<const float*>(lds + 4 * TILE + (2 + buf) * STAT);
-        tile(hq, qbase, lds + buf * TILE, lds + (2 + buf) * TILE, lsel, dltl, masked_c);
-      }
       stat_k();
     }
     wait_vmem();

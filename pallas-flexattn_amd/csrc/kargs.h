@@ -110,6 +110,19 @@ __device__ __forceinline__ float score_t(const Problem& p, float raw, float slop
   }
 }
 
+// score_t<true> without branches, for straight-line tile schedules: the
+// soft-cap's tanh is always evaluated and selected (cap_inv = 1 / softcap, or
+// 0 without a soft-cap; slope 0 without ALiBi).
+__device__ __forceinline__ float score_mods_flat(float raw, float scale, float slope, int q, int k, float softcap,
+                                                 float cap_inv, float* dsdx) {
+  float s = fmaf(slope, (float)(k - q), raw * scale);
+  const float th = tanh_fast(s * cap_inv);
+  const bool capped = softcap > 0.f;
+  *dsdx = capped ? fmaf(-th, th, 1.0f) : 1.0f;
+  s = capped ? softcap * th : s;
+  return s * kLog2e;
+}
+
 // Tile start used for out-of-range table entries: beyond any sequence, so the
 // tile is skipped and its loads are predicated off.
 constexpr int kPastEnd = 0x40000000;
