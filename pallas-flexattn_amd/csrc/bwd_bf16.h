@@ -180,6 +180,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
   const float lse2 = qvalid ? a.lse[rowi] * kLog2e : INFINITY;
   const float dl = qvalid ? a.delta[rowi] : 0.f;
   const float slope = P.alibi ? P.alibi[h] : 0.f;
+  const float cap_inv = P.softcap > 0.f ? 1.0f / P.softcap : 0.f;
   int klo, khi;  // keys visible to this lane's query (masks are intervals here)
   key_interval(P, b, qw, &klo, &khi);
 
@@ -244,7 +245,8 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
       for (int e = 0; e < 16; ++e) {
         dsdx[e] = 1.f;
         if constexpr (kMods)
-          sacc[e] = score_t<true>(P, sacc[e], slope, qw, kbase + 32 * j + acc_row(e, hh), &dsdx[e]);
+          sacc[e] = score_mods_flat(sacc[e], P.scale, slope, qw, kbase + 32 * j + acc_row(e, hh), P.softcap, cap_inv,
+                                    &dsdx[e]);
       }
       if constexpr (kMasked) {
 #pragma unroll

@@ -78,6 +78,7 @@ void fwd_bf16_kernel(FwdArgs a) {
     for (int s = 0; s < KSTEPS; ++s) qf[s] = buf_load16(rq, qw * RB + (2 * s + hh) * 16);
   }
   const float slope = P.alibi ? P.alibi[h] : 0.f;
+  const float cap_inv = P.softcap > 0.f ? 1.0f / P.softcap : 0.f;
   // every mask term is an interval of keys per query (the host routes
   // arbitrary document labels to the generic kernel)
   int klo, khi;
@@ -254,8 +255,11 @@ void fwd_bf16_kernel(FwdArgs a) {
 #pragma unroll
         for (int j = 0; j < NSUB; ++j)
 #pragma unroll
-          for (int e = 0; e < 16; ++e)
-            sacc[j][e] = score_t<true>(P, sacc[j][e], slope, qw, kbase + 32 * j + acc_row(e, hh), nullptr);
+          for (int e = 0; e < 16; ++e) {
+            float dsdx;  // unused in the forward
+            sacc[j][e] = score_mods_flat(sacc[j][e], P.scale, slope, qw, kbase + 32 * j + acc_row(e, hh), P.softcap,
+                                         cap_inv, &dsdx);
+          }
       }
       if (masked) {  // partial tile: keys outside [klo, khi] are dropped
 #pragma unroll
