@@ -13,6 +13,10 @@
  *             dQ :313-407): dQ, dK, dV.
  *   fa_bwd_workspace_bytes — scratch size for fa_bwd (XLA allocated the
  *             reference's intermediates, e.g. the Delta array of :188-202).
+ *   fa_mask_build_workspace_bytes / fa_build_block_mask — create_block_mask
+ *             (block_mask.py:54-129) for window / document masks, evaluated
+ *             on the device: the reference's sampled fields and the kernels'
+ *             exact tables.
  *   fa_strerror / fa_abi_version — error text and ABI version for the
  *             binding layer (no reference counterpart: the reference raised
  *             Python exceptions at trace time).
@@ -118,6 +122,47 @@ int fa_bwd_dkdv(const fa_params *p, const void *q, const void *k, const void *v,
                 const float *lse, const float *delta, void *dk, void *dv, void *stream);
 int fa_bwd_dq(const fa_params *p, const void *q, const void *k, const void *v, const void *dout,
               const float *lse, const float *delta, void *dq, void *stream);
+
+/*
+ * Block-mask construction on the device (create_block_mask, block_mask.py:54-129)
+ * for the mask semantics of fa_params: the window (window_left, window_right)
+ * and, optionally, document ids shared by queries and keys (token t of table
+ * row r has id doc_ids[r][t]).  Blocks are `block` tokens (the last one of each
+ * side may be shorter); nq = ceil(q_len / block), nk = ceil(kv_len / block).
+ * For table row r, query block i and key block j:
+ *   sampled — the reference's rule (block_mask.py:85-109): kept iff the mask
+ *             holds at one of the 3x3 points {s, (s+e)/2, e-1} x {s', (s'+e')/2, e'-1}
+ *             ([s, e) and [s', e') the blocks' token ranges);
+ *   live    — some element of the tile is kept;
+ *   full    — all block x block elements are kept (so none lies past either
+ *             sequence end).
+ * Outputs (device int32; rows ascending, padded with -1 to the full width):
+ *   sampled_num (rows, nq), sampled_indices (rows, nq, nk)      the reference's
+ *             num_blocks_in_row / col_indices;
+ *   kv_num_blocks / kv_indices (rows, nq) / (rows, nq, nk)      live && !full;
+ *   full_kv_num_blocks / full_kv_indices                        full;
+ *   q_num_blocks / q_indices (rows, nk) / (rows, nk, nq)        transposed, live && !full;
+ *   full_q_num_blocks / full_q_indices                          transposed, full;
+ *   max_counts[5]  the largest row count of the five lists, in this order.
+ * The kv/q tables serve as fa_params tables with mask_block_q = mask_block_kv
+ * = block, kv_width = nk, q_width = nq, table_b = rows, table_h = 1. */
+typedef struct fa_mask_build {
+  int32_t abi_version; /* FA_ABI_VERSION */
+  int32_t rows;        /* table rows (>= 1): the rows of doc_ids, or 1 */
+  int32_t q_len, kv_len, block;
+  int32_t window_left, window_right;
+  const int32_t *doc_ids; /* (rows, doc_len) or NULL */
+  int32_t doc_len;        /* >= max(q_len, kv_len) when doc_ids is set */
+  int32_t *sampled_num, *sampled_indices;
+  int32_t *kv_num_blocks, *kv_indices, *full_kv_num_blocks, *full_kv_indices;
+  int32_t *q_num_blocks, *q_indices, *full_q_num_blocks, *full_q_indices;
+  int32_t *max_counts;
+} fa_mask_build;
+
+/* Bytes of device scratch fa_build_block_mask needs (tile flags, block ids). */
+size_t fa_mask_build_workspace_bytes(const fa_mask_build *m);
+
+int fa_build_block_mask(const fa_mask_build *m, void *workspace, size_t workspace_bytes, void *stream);
 
 const char *fa_strerror(int status);
 int fa_abi_version(void);

@@ -6,6 +6,7 @@
 #include "bwd.h"
 #include "bwd_bf16.h"
 #include "fwd_bf16.h"
+#include "mask_build.h"
 
 namespace {
 
@@ -217,6 +218,29 @@ size_t delta_bytes(const fa_params* p) {
   return ((size_t)p->B * p->Hq * p->Sq * sizeof(float) + 255) & ~(size_t)255;
 }
 
+// ------------------------------------------------------ block masks ----
+struct MaskLayout {
+  int nq, nk;
+  size_t flags_bytes, qdoc_off, kdoc_off, total;
+};
+
+int mask_layout(const fa_mask_build* m, MaskLayout* L) {
+  if (!m) return FA_ERR_NULL;
+  if (m->abi_version != FA_ABI_VERSION) return FA_ERR_VERSION;
+  if (m->rows < 1 || m->q_len < 1 || m->kv_len < 1 || m->block < 1) return FA_ERR_SHAPE;
+  if (m->doc_ids && m->doc_len < (m->q_len > m->kv_len ? m->q_len : m->kv_len)) return FA_ERR_SHAPE;
+  if (!m->doc_ids && m->rows != 1) return FA_ERR_SHAPE;
+  L->nq = cdiv(m->q_len, m->block);
+  L->nk = cdiv(m->kv_len, m->block);
+  if (L->nq + L->nk > 65535 || m->rows > 65535) return FA_ERR_SHAPE;
+  auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  L->flags_bytes = up((size_t)m->rows * L->nq * L->nk);
+  L->qdoc_off = L->flags_bytes;
+  L->kdoc_off = L->qdoc_off + up((size_t)m->rows * L->nq * 4);
+  L->total = L->kdoc_off + up((size_t)m->rows * L->nk * 4);
+  return FA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -326,6 +350,53 @@ int fa_bwd_dq(const fa_params* p, const void* q, const void* k, const void* v, c
   a.delta = const_cast<float*>(delta);
   a.dq = dq;
   return bwd_stages(p, a, kStageDq, static_cast<hipStream_t>(stream));
+}
+
+size_t fa_mask_build_workspace_bytes(const fa_mask_build* m) {
+  MaskLayout L;
+  return mask_layout(m, &L) == FA_OK ? L.total : 0;
+}
+
+int fa_build_block_mask(const fa_mask_build* m, void* workspace, size_t workspace_bytes, void* stream) {
+  MaskLayout L;
+  const int rc = mask_layout(m, &L);
+  if (rc != FA_OK) return rc;
+  int32_t* outs[] = {m->sampled_num, m->sampled_indices, m->kv_num_blocks, m->kv_indices, m->full_kv_num_blocks,
+                     m->full_kv_indices, m->q_num_blocks, m->q_indices, m->full_q_num_blocks, m->full_q_indices,
+                     m->max_counts};
+  for (int32_t* o : outs)
+    if (!o) return FA_ERR_NULL;
+  if (!workspace || workspace_bytes < L.total) return FA_ERR_WORKSPACE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  fa::MaskBuild b;
+  b.rows = m->rows;
+  b.q_len = m->q_len;
+  b.kv_len = m->kv_len;
+  b.block = m->block;
+  b.nq = L.nq;
+  b.nk = L.nk;
+  b.left = m->window_left < 0 ? -1 : m->window_left;
+  b.right = m->window_right < 0 ? -1 : m->window_right;
+  b.doc = m->doc_ids;
+  b.doc_len = m->doc_len;
+  b.flags = reinterpret_cast<uint8_t*>(ws);
+  b.qdoc = reinterpret_cast<int32_t*>(ws + L.qdoc_off);
+  b.kdoc = reinterpret_cast<int32_t*>(ws + L.kdoc_off);
+  hipLaunchKernelGGL(fa::mb_zero, dim3(1), dim3(64), 0, s, m->max_counts, 5);
+  if (b.doc)
+    hipLaunchKernelGGL(fa::mb_block_docs, dim3(b.rows, L.nq > L.nk ? L.nq : L.nk), dim3(64), 0, s, b);
+  hipLaunchKernelGGL(fa::mb_classify, dim3(b.rows, L.nq), dim3(256), 0, s, b);
+  fa::CompactArgs c;
+  c.m = b;
+  // sampled (bit 2), kv partial (live, not full), kv full; q partial, q full
+  c.lists[0] = {m->sampled_num, m->sampled_indices, m->max_counts + 0, 4, 4};
+  c.lists[1] = {m->kv_num_blocks, m->kv_indices, m->max_counts + 1, 3, 1};
+  c.lists[2] = {m->full_kv_num_blocks, m->full_kv_indices, m->max_counts + 2, 2, 2};
+  c.lists[3] = {m->q_num_blocks, m->q_indices, m->max_counts + 3, 3, 1};
+  c.lists[4] = {m->full_q_num_blocks, m->full_q_indices, m->max_counts + 4, 2, 2};
+  hipLaunchKernelGGL(fa::mb_compact, dim3(b.rows, L.nq > L.nk ? L.nq : L.nk, 5), dim3(256), 0, s, c);
+  return launch_status();
 }
 
 }  // extern "C"

@@ -40,8 +40,24 @@ class FaParams(ctypes.Structure):
     ]
 
 
+class FaMaskBuild(ctypes.Structure):
+    """Mirror of ``struct fa_mask_build`` (include/flexattn.h)."""
+    _fields_ = [
+        ("abi_version", _i32), ("rows", _i32),
+        ("q_len", _i32), ("kv_len", _i32), ("block", _i32),
+        ("window_left", _i32), ("window_right", _i32),
+        ("doc_ids", _pi32), ("doc_len", _i32),
+        ("sampled_num", _pi32), ("sampled_indices", _pi32),
+        ("kv_num_blocks", _pi32), ("kv_indices", _pi32),
+        ("full_kv_num_blocks", _pi32), ("full_kv_indices", _pi32),
+        ("q_num_blocks", _pi32), ("q_indices", _pi32),
+        ("full_q_num_blocks", _pi32), ("full_q_indices", _pi32),
+        ("max_counts", _pi32),
+    ]
+
+
 EXPORTED = ("fa_fwd", "fa_bwd", "fa_bwd_workspace_bytes", "fa_bwd_preprocess", "fa_bwd_dkdv", "fa_bwd_dq",
-            "fa_strerror", "fa_abi_version")
+            "fa_mask_build_workspace_bytes", "fa_build_block_mask", "fa_strerror", "fa_abi_version")
 
 _lib = None
 
@@ -74,6 +90,11 @@ def load():
     lib.fa_bwd_dq.restype = ctypes.c_int
     lib.fa_bwd_workspace_bytes.argtypes = [P]
     lib.fa_bwd_workspace_bytes.restype = ctypes.c_size_t
+    M = ctypes.POINTER(FaMaskBuild)
+    lib.fa_mask_build_workspace_bytes.argtypes = [M]
+    lib.fa_mask_build_workspace_bytes.restype = ctypes.c_size_t
+    lib.fa_build_block_mask.argtypes = [M, v, ctypes.c_size_t, v]
+    lib.fa_build_block_mask.restype = ctypes.c_int
     lib.fa_strerror.argtypes = [ctypes.c_int]
     lib.fa_strerror.restype = ctypes.c_char_p
     lib.fa_abi_version.argtypes = []

@@ -265,6 +265,70 @@ def _finish(num, col, mask_mod, B, H, Q_LEN, KV_LEN, block_size, kernel_block=No
                      q_len=Q_LEN, kv_len=KV_LEN, mask_mod=mask_mod, **kernel_tables(live, full))
 
 
+_TABLE_NAMES = ("kv_num_blocks", "kv_indices", "full_kv_num_blocks", "full_kv_indices",
+                "q_num_blocks", "q_indices", "full_q_num_blocks", "full_q_indices")
+
+
+def _build_on_device(spec: MaskSpec, q_len: int, kv_len: int, bs: int, device):
+    """Evaluate the block mask of a mask descriptor on the GPU (C ABI
+    ``fa_build_block_mask``).  Returns the sampled (num, col) fields shaped
+    (rows, 1, ...), the kernel tables (host arrays) and their device copies.
+    All outputs live in one device buffer, copied to the host at once."""
+    import ctypes
+    import torch
+    from . import _lib
+    lib = _lib.load()
+    dev = torch.device(device)
+    rows = spec.doc_ids.shape[0] if spec.doc_ids is not None else 1
+    nq, nk = math.ceil(q_len / bs), math.ceil(kv_len / bs)
+    docs = None
+    if spec.doc_ids is not None:
+        if spec.doc_ids.shape[1] < max(q_len, kv_len):
+            raise ValueError("doc_ids shorter than the sequence")
+        docs = torch.from_numpy(spec.doc_ids).to(dev)
+    shapes = {"sampled_num": (rows, nq), "sampled_indices": (rows, nq, nk)}
+    for side, n, m in (("kv", nq, nk), ("q", nk, nq)):
+        for prefix in ("", "full_"):
+            shapes[f"{prefix}{side}_num_blocks"] = (rows, n)
+            shapes[f"{prefix}{side}_indices"] = (rows, n, m)
+    shapes["max_counts"] = (5,)
+    sizes = {k: int(np.prod(v)) for k, v in shapes.items()}
+    buf = torch.empty(sum(sizes.values()), dtype=torch.int32, device=dev)
+    views, off = {}, 0
+    for k, v in shapes.items():
+        views[k] = buf[off:off + sizes[k]].view(v)
+        off += sizes[k]
+    args = _lib.FaMaskBuild(abi_version=_lib.ABI_VERSION, rows=rows, q_len=q_len, kv_len=kv_len, block=bs,
+                            window_left=spec.left, window_right=spec.right,
+                            doc_ids=docs.data_ptr() if docs is not None else None,
+                            doc_len=int(spec.doc_ids.shape[1]) if docs is not None else 0,
+                            **{k: t.data_ptr() for k, t in views.items()})
+    ws_bytes = lib.fa_mask_build_workspace_bytes(ctypes.byref(args))
+    if ws_bytes == 0:
+        raise ValueError("fa_build_block_mask: sizes out of range")
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    _lib.check(lib.fa_build_block_mask(ctypes.byref(args), ws.data_ptr(), ws_bytes, stream))
+    host = buf.cpu().numpy()  # synchronizes
+    hv, off = {}, 0
+    for k, v in shapes.items():
+        hv[k] = host[off:off + sizes[k]].reshape(v)
+        off += sizes[k]
+    mc = hv["max_counts"]
+    wk, wq = max(1, int(mc[1]), int(mc[2])), max(1, int(mc[3]), int(mc[4]))
+    tables, dev_tables = {}, {}
+    for name in _TABLE_NAMES:
+        t, h = views[name], hv[name]
+        if t.dim() == 3:
+            w = wk if name.endswith("kv_indices") else wq
+            t, h = t[..., :w], h[..., :w]
+        dev_tables[name] = t.unsqueeze(1).contiguous()
+        tables[name] = np.ascontiguousarray(h[:, None])
+    num = np.ascontiguousarray(hv["sampled_num"][:, None])
+    col = np.ascontiguousarray(hv["sampled_indices"][..., :int(mc[0])][:, None])
+    return num, col, tables, dev_tables
+
+
 def create_block_mask(
     mask_mod: MaskMod,
     B: int,
@@ -272,13 +336,25 @@ def create_block_mask(
     Q_LEN: int,
     KV_LEN: int,
     block_size: int = 128,
+    device=None,
 ) -> BlockMask:
     """Create a BlockMask from a mask_mod (``block_mask.py:54-129``).
 
     The reference fields follow the reference's 3x3 sampling rule exactly.
     The kernel tables classify every element; if the sampled rule misses a
     block that has live elements, a warning is issued (the kernels use the
-    exact tables)."""
+    exact tables).  With ``device`` (a GPU) and a mask descriptor
+    (:class:`MaskSpec`), both are evaluated on the device by the HIP
+    library, with identical results, and the tables stay cached there."""
+    if device is not None and isinstance(mask_mod, MaskSpec):
+        num, col, tables, dev_tables = _build_on_device(mask_mod, Q_LEN, KV_LEN, block_size, device)
+        if num.shape[0] == 1:
+            num, col = num[0, 0], col[0, 0]
+        bm = BlockMask(num_blocks_in_row=np.ascontiguousarray(num), col_indices=np.ascontiguousarray(col),
+                       block_size=block_size, q_len=Q_LEN, kv_len=KV_LEN, mask_mod=mask_mod, **tables)
+        bm._device_cache[str(device)] = dev_tables
+        _warn_if_sampling_misses(int(np.sum(num)), bm)
+        return bm
     tb, th = _mask_dims(mask_mod, B, H)
     sampled = np.stack([np.stack([_sampled_live(mask_mod, b, h, Q_LEN, KV_LEN, block_size)
                                   for h in range(th)]) for b in range(tb)])
@@ -286,12 +362,16 @@ def create_block_mask(
     if tb == 1 and th == 1:
         num, col = num[0, 0], col[0, 0]
     bm = _finish(np.ascontiguousarray(num), np.ascontiguousarray(col), mask_mod, B, H, Q_LEN, KV_LEN, block_size)
-    exact_live = (bm.kv_num_blocks + bm.full_kv_num_blocks).sum()
-    if exact_live != sampled.sum():
-        warnings.warn("create_block_mask: the 3x3 sampling rule and the exact classification disagree "
-                      f"({int(sampled.sum())} vs {int(exact_live)} live blocks); kernels use the exact tables",
-                      stacklevel=2)
+    _warn_if_sampling_misses(int(sampled.sum()), bm)
     return bm
+
+
+def _warn_if_sampling_misses(sampled_live: int, bm: BlockMask) -> None:
+    exact_live = int((bm.kv_num_blocks + bm.full_kv_num_blocks).sum())
+    if exact_live != sampled_live:
+        warnings.warn("create_block_mask: the 3x3 sampling rule and the exact classification disagree "
+                      f"({sampled_live} vs {exact_live} live blocks); kernels use the exact tables",
+                      stacklevel=3)
 
 
 def _closed_form(rows, n):

@@ -27,7 +27,7 @@ from typing import Optional, Tuple
 import numpy as np
 
 from . import _lib
-from .block_mask import BlockMask, _finish
+from .block_mask import BlockMask, _finish, create_block_mask
 from .kernel_tuner import (DEFAULT_BLOCK_C, DEFAULT_BLOCK_R, DEFAULT_NUM_STAGES, DEFAULT_NUM_WARPS,
                            kernel_tiles, tuned_tiles)
 from .mask_mod import MaskSpec, MaskMod
@@ -151,11 +151,16 @@ class _Plan:
 _MASK_CACHE = {}
 
 
-def _internal_block_mask(mask: MaskSpec, B: int, Sq: int, Skv: int) -> BlockMask:
-    key = (mask.key(), B, Sq, Skv)
+def _internal_block_mask(mask: MaskSpec, B: int, Sq: int, Skv: int, device=None) -> BlockMask:
+    """Tables for a mask given without a BlockMask, built on ``device`` when it is a GPU."""
+    on_gpu = device is not None and getattr(device, "type", str(device)) == "cuda"
+    key = (mask.key(), B, Sq, Skv, str(device) if on_gpu else None)
     bm = _MASK_CACHE.get(key)
     if bm is None:
-        bm = _finish(None, None, mask, B, 1, Sq, Skv, TABLE_BLOCK)
+        if on_gpu:
+            bm = create_block_mask(mask, B, 1, Sq, Skv, TABLE_BLOCK, device=device)
+        else:
+            bm = _finish(None, None, mask, B, 1, Sq, Skv, TABLE_BLOCK)
         if len(_MASK_CACHE) > 64:
             _MASK_CACHE.clear()
         _MASK_CACHE[key] = bm
@@ -198,7 +203,7 @@ def _fwd_core(q, k, v, mask, score, scale, block_mask, tiles):
     _check_inputs(q, k, v)
     q, k, v = _dense16(q), _dense16(k), _dense16(v)
     if block_mask is None and mask is not None and not mask.is_trivial:
-        block_mask = _internal_block_mask(mask, q.shape[0], q.shape[2], k.shape[2])
+        block_mask = _internal_block_mask(mask, q.shape[0], q.shape[2], k.shape[2], q.device)
     plan = _Plan(q, k, mask, score, scale, block_mask, tiles)
     o = torch.empty_like(q)
     lse = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
@@ -218,7 +223,7 @@ def _bwd_core(q, k, v, o, lse, do, mask, score, scale, block_mask, tiles):
     if o.shape != q.shape or do.shape != q.shape or lse.shape != q.shape[:3]:
         raise ValueError("o / do / lse shapes do not match q")
     if block_mask is None and mask is not None and not mask.is_trivial:
-        block_mask = _internal_block_mask(mask, q.shape[0], q.shape[2], k.shape[2])
+        block_mask = _internal_block_mask(mask, q.shape[0], q.shape[2], k.shape[2], q.device)
     plan = _Plan(q, k, mask, score, scale, block_mask, tiles)
     lib = _lib.load()
     ws_bytes = lib.fa_bwd_workspace_bytes(plan.ptr())
@@ -246,7 +251,7 @@ def _stage_plan(q4, k4, mask_mod, block_r, block_c, scale=None):
     mask = _as_mask_spec(mask_mod)
     bm = None
     if mask is not None and not mask.is_trivial:
-        bm = _internal_block_mask(mask, q4.shape[0], q4.shape[2], k4.shape[2])
+        bm = _internal_block_mask(mask, q4.shape[0], q4.shape[2], k4.shape[2], q4.device)
     return _Plan(q4, k4, mask, None, scale, bm, _ref_tiles(q4, block_r, block_c))
 
 
@@ -321,7 +326,7 @@ class Runner:
         self.do = _dense16(do)
         mask = _as_mask_spec(mask_mod if block_mask is None else block_mask.mask_mod)
         if block_mask is None and mask is not None and not mask.is_trivial:
-            block_mask = _internal_block_mask(mask, q.shape[0], q.shape[2], k.shape[2])
+            block_mask = _internal_block_mask(mask, q.shape[0], q.shape[2], k.shape[2], q.device)
         _, dname = _dtype_code(q)
         tiles = tiles or (128, 64 if dname == "bf16" else 32)
         self.plan = _Plan(self.q, self.k, mask, _as_score_spec(score_mod), scale, block_mask, tiles)
@@ -456,7 +461,7 @@ def flex_attention(query, key, value, score_mod: Optional[ScoreSpec] = None,
             raise ValueError("block_mask has no kernel tables (build it with create_block_mask)")
         if block_mask.block_size % TABLE_BLOCK and mask is not None:
             # the dK/dV kernel walks 128-key tiles: re-derive the exact tables at 128
-            block_mask = _internal_block_mask(mask, query.shape[0], query.shape[2], key.shape[2])
+            block_mask = _internal_block_mask(mask, query.shape[0], query.shape[2], key.shape[2], query.device)
     _, dname = _dtype_code(query)
     opts = kernel_options or {}
     tiles = None

@@ -74,3 +74,54 @@ def test_null_pointers_and_small_workspace_rejected():
     assert need >= 2 * 128 * 4
     assert lib.fa_bwd(ctypes.byref(p), d, d, d, d, d, d, d, d, d, d, need - 1, None) == -6
     assert lib.fa_bwd_dq(ctypes.byref(p), d, d, d, d, d, None, d, None) == -1
+
+
+def _mask_build(**kw):
+    m = _lib.FaMaskBuild()
+    m.abi_version = _lib.ABI_VERSION
+    m.rows, m.q_len, m.kv_len, m.block = 1, 1000, 1000, 128
+    m.window_left, m.window_right = -1, 0
+    for name, _ in _lib.FaMaskBuild._fields_:
+        if name.endswith(("_num", "_indices", "_blocks", "max_counts")):
+            setattr(m, name, 16)
+    for k, v in kw.items():
+        setattr(m, k, v)
+    return m
+
+
+def test_mask_build_workspace_layout():
+    lib = _lib.load()
+    # flags (1 x 8 x 8 bytes), then the two block-document arrays, each rounded up to 256 bytes
+    assert lib.fa_mask_build_workspace_bytes(ctypes.byref(_mask_build())) == 3 * 256
+    m = _mask_build(rows=2, doc_ids=16, doc_len=1000, q_len=1000, kv_len=600, block=64)
+    assert lib.fa_mask_build_workspace_bytes(ctypes.byref(m)) == 512 + 256 + 256
+    assert lib.fa_mask_build_workspace_bytes(ctypes.byref(_mask_build(block=0))) == 0
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(abi_version=99), -8), (dict(q_len=0), -2), (dict(block=0), -2),
+    (dict(rows=2), -2),                                  # several table rows need document ids
+    (dict(doc_ids=16, doc_len=999), -2),                 # ids shorter than the sequences
+    (dict(q_len=64 * 65535, block=64), -2),              # too many blocks for one launch
+    (dict(kv_indices=None), -1), (dict(max_counts=None), -1),
+])
+def test_mask_build_rejects_bad_arguments_before_any_launch(kw, code):
+    lib = _lib.load()
+    m = _mask_build(**kw)
+    assert lib.fa_build_block_mask(ctypes.byref(m), ctypes.c_void_p(16), 1 << 20, None) == code
+
+
+def test_mask_build_null_struct_and_small_workspace_rejected():
+    lib = _lib.load()
+    assert lib.fa_build_block_mask(None, ctypes.c_void_p(16), 1 << 20, None) == -1
+    m = _mask_build()
+    need = lib.fa_mask_build_workspace_bytes(ctypes.byref(m))
+    assert lib.fa_build_block_mask(ctypes.byref(m), ctypes.c_void_p(16), need - 1, None) == -6
+    assert lib.fa_build_block_mask(ctypes.byref(m), None, need, None) == -6
+
+
+def test_mask_build_struct_layout_matches_header():
+    m = _lib.FaMaskBuild
+    # 7 int32, then the ids pointer (8-byte aligned), doc_len, then 11 pointers
+    assert m.doc_ids.offset == 32 and m.doc_len.offset == 40 and m.sampled_num.offset == 48
+    assert ctypes.sizeof(m) == m.max_counts.offset + 8 == 48 + 11 * 8
