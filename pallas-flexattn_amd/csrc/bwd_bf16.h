@@ -159,7 +159,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
   const int lr = lane & 31, hh = lane >> 5;
   const int nqt = (P.Sq + BM - 1) / BM;
   int head, qt;
-  work_item(blockIdx.x, P.B * P.Hq, nqt, P.xcd_remap, &head, &qt);
+  work_item(blockIdx.x, P.B * P.Hq, nqt, P.xcd_remap, P.head_group_q, false, &head, &qt);
   const int b = head / P.Hq, h = head - b * P.Hq;
   const int hk = h / (P.Hq / P.Hkv);
   const int q0 = qt * BM;
@@ -354,7 +354,7 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   const int nkt = (P.Skv + BKV - 1) / BKV;
   const int g = P.Hq / P.Hkv;
   int head, kt;
-  work_item(blockIdx.x, P.B * P.Hkv, nkt, P.xcd_remap, &head, &kt);
+  work_item(blockIdx.x, P.B * P.Hkv, nkt, P.xcd_remap, P.head_group_kv, true, &head, &kt);
   const int b = head / P.Hkv, hk = head - b * P.Hkv;
   const int k0 = kt * BKV;
   const int kw = k0 + 32 * w + lr;

@@ -38,6 +38,20 @@ int default_tiles(const fa_params* p, Tiles* t) {
 
 inline int cdiv(int a, int b) { return (a + b - 1) / b; }
 
+// Byte budgets of a head group: the L2 of one XCD is 4 MiB; q-tile walks
+// (forward, dQ) measured best at twice that (the misses hit the MALL and the
+// wider level-major groups balance the grid's tail), kv-tile walks (dK/dV) at
+// the L2 size.
+constexpr size_t kGroupBytesQ = 8u << 20;
+constexpr size_t kGroupBytesKV = 4u << 20;
+// largest power of two g dividing the heads of one XCD with g * bytes <= budget
+int head_group(int nheads, size_t bytes_per_head, size_t budget) {
+  const int hpx = nheads % 8 == 0 ? nheads / 8 : 1;
+  int g = 1;
+  while (hpx % (2 * g) == 0 && (size_t)(2 * g) * bytes_per_head <= budget) g *= 2;
+  return g;
+}
+
 int build_problem(const fa_params* p, const Tiles& t, Problem* pr) {
   if (!p) return FA_ERR_NULL;
   if (p->abi_version != FA_ABI_VERSION) return FA_ERR_VERSION;
@@ -67,6 +81,15 @@ int build_problem(const fa_params* p, const Tiles& t, Problem* pr) {
   r.softcap = p->softcap;
   r.has_mask = (r.win_left >= 0 || r.win_right >= 0 || r.q_doc != nullptr) ? 1 : 0;
   r.xcd_remap = 1;
+  // heads per level-major group: as many as keep their K/V (forward, dQ) or
+  // Q/dO (dK/dV, all q heads of a kv head) within the group budget
+  {
+    const size_t es = p->dtype == FA_DTYPE_BF16 ? 2 : 4;
+    const size_t kv_head = 2 * (size_t)p->Skv * p->D * es / (size_t)(p->Hq / p->Hkv);
+    const size_t q_heads = 2 * (size_t)p->Sq * p->D * es * (size_t)(p->Hq / p->Hkv);
+    r.head_group_q = head_group(p->B * p->Hq, kv_head, kGroupBytesQ);
+    r.head_group_kv = head_group(p->B * p->Hkv, q_heads, kGroupBytesKV);
+  }
   r.kv_num = p->kv_num_blocks;
   r.kv_idx = p->kv_indices;
   r.full_kv_num = p->full_kv_num_blocks;

@@ -105,7 +105,7 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdArgs a) {
   const int lr = lane & 31, hh = lane >> 5;
   const int nqt = (P.Sq + BM - 1) / BM;
   int head, qt;
-  work_item(blockIdx.x, P.B * P.Hq, nqt, P.xcd_remap, &head, &qt);
+  work_item(blockIdx.x, P.B * P.Hq, nqt, P.xcd_remap, P.head_group_q, false, &head, &qt);
   const int b = head / P.Hq, h = head - b * P.Hq;
   const int hk = h / (P.Hq / P.Hkv);
   const int q0 = qt * BM;

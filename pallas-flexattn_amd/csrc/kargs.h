@@ -33,6 +33,8 @@ struct Problem {
   int has_tables;        // 0: dense iteration over all blocks
   int has_mask;          // any window / doc term active
   int xcd_remap;         // group work of a head onto one XCD
+  int head_group_q;      // heads per level-major group, q-tile walks (forward, dQ)
+  int head_group_kv;     // the same for kv-tile walks (dK/dV)
 };
 
 // Window part of the element mask (q, kv inside the sequence bounds).
@@ -137,20 +139,27 @@ __device__ __forceinline__ int tab_row(const Problem& p, int b, int h, int row, 
 }
 
 // Work-item order: blockIdx.x is dispatched round-robin over the 8 XCDs.  With
-// remapping, XCD x processes heads [x*H/8, (x+1)*H/8) one after another, each
-// head's tiles in reverse order (longest causal rows first), so the K/V (or
-// Q/dO) of a head stay in that XCD's L2 while its tiles run.
-__device__ __forceinline__ void work_item(int bid, int nheads, int ntiles, bool remap, int* head,
-                                          int* tile) {
+// remapping, XCD x processes heads [x*H/8, (x+1)*H/8) in groups of `group`
+// heads, one group after another, so the K/V (or Q/dO) of a group stay in
+// that XCD's L2 while its tiles run (the host sizes groups to the L2).  Inside
+// a group the tiles go level by level across its heads, the longest walks
+// first (causal: the last q tiles, or with low_first the first kv tiles), so
+// the short tiles fill the end of the grid.
+__device__ __forceinline__ void work_item(int bid, int nheads, int ntiles, bool remap, int group, bool low_first,
+                                          int* head, int* tile) {
+  int t;
   if (remap && (nheads % 8) == 0) {
     const int xcd = bid & 7, slot = bid >> 3;
     const int hpx = nheads >> 3;
-    *head = xcd * hpx + slot / ntiles;
-    *tile = ntiles - 1 - (slot % ntiles);
+    const int per_group = group * ntiles;
+    const int gi = slot / per_group, r = slot - gi * per_group;
+    *head = xcd * hpx + gi * group + r % group;
+    t = r / group;
   } else {
     *head = bid / ntiles;
-    *tile = ntiles - 1 - (bid % ntiles);
+    t = bid % ntiles;
   }
+  *tile = low_first ? t : ntiles - 1 - t;
 }
 
 }  // namespace fa
