@@ -128,7 +128,7 @@ int fa_bwd_dq(const fa_params *p, const void *q, const void *k, const void *v, c
  * for the mask semantics of fa_params: the window (window_left, window_right)
  * and, optionally, document ids shared by queries and keys (token t of table
  * row r has id doc_ids[r][t]).  Blocks are `block` tokens (the last one of each
- * side may be shorter); nq = ceil(q_len / block), nk = ceil(kv_len / block).
+ * side may be shorter; 1 <= block <= 1024); nq = ceil(q_len / block), nk = ceil(kv_len / block).
  * For table row r, query block i and key block j:
  *   sampled — the reference's rule (block_mask.py:85-109): kept iff the mask
  *             holds at one of the 3x3 points {s, (s+e)/2, e-1} x {s', (s'+e')/2, e'-1}

@@ -250,7 +250,8 @@ struct MaskLayout {
 int mask_layout(const fa_mask_build* m, MaskLayout* L) {
   if (!m) return FA_ERR_NULL;
   if (m->abi_version != FA_ABI_VERSION) return FA_ERR_VERSION;
-  if (m->rows < 1 || m->q_len < 1 || m->kv_len < 1 || m->block < 1) return FA_ERR_SHAPE;
+  if (m->rows < 1 || m->q_len < 1 || m->kv_len < 1 || m->block < 1 || m->block > fa::kMaxMaskBlock)
+    return FA_ERR_SHAPE;
   if (m->doc_ids && m->doc_len < (m->q_len > m->kv_len ? m->q_len : m->kv_len)) return FA_ERR_SHAPE;
   if (!m->doc_ids && m->rows != 1) return FA_ERR_SHAPE;
   L->nq = cdiv(m->q_len, m->block);

@@ -8,8 +8,10 @@
 //                  (block_mask.py:85-109) and the exact live / full state.
 //                  Windows are intervals on q - kv, so most tiles resolve from
 //                  the tile's corners; with documents, tiles whose two blocks
-//                  each lie in one document compare the two ids, and only
-//                  tiles crossing a document boundary test every element;
+//                  each lie in one document compare the two ids, a tile with
+//                  one such block tests each element of the other block
+//                  against the window's interval, and only tiles whose two
+//                  blocks both cross a document boundary test every element;
 //   mb_compact     per table row (one workgroup): ascending index lists of
 //                  the selected tiles by a ballot scan, padded with -1, and
 //                  the row's count folded into a running maximum.
@@ -67,8 +69,11 @@ __global__ __launch_bounds__(64) void mb_block_docs(MaskBuild m) {
   }
 }
 
+constexpr int kMaxMaskBlock = 1024;
+
 // grid: (rows, nq); 256 threads, wave w takes the tiles j = w, w + 4, ...
 __global__ __launch_bounds__(256) void mb_classify(MaskBuild m) {
+  __shared__ int kd_lds[4][kMaxMaskBlock];
   const int row = blockIdx.x, i = blockIdx.y;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int32_t* doc_row = m.doc ? m.doc + (size_t)row * m.doc_len : nullptr;
@@ -103,9 +108,43 @@ __global__ __launch_bounds__(256) void mb_classify(MaskBuild m) {
       if (qd != kMixedDoc && kd != kMixedDoc) {
         live = qd == kd;
         full = live && wfull && complete;
+      } else if (kd != kMixedDoc || qd != kMixedDoc) {
+        // one block lies in one document: per element of the other block
+        // (lanes take them), same id or not, and if so the window's interval
+        // over the uniform block
+        const bool q_side = kd != kMixedDoc;  // lanes walk the query rows
+        const int uni = q_side ? kd : qd;
+        const int a0 = q_side ? qa : ka, a1 = q_side ? qe : ke;  // walked block [a0, a1)
+        const int b0 = q_side ? ka : qa, b1 = (q_side ? ke : qe) - 1;  // uniform block [b0, b1]
+        bool any = false, all = complete;
+        for (int r = lane; r < m.block; r += 64) {
+          const int x = a0 + r;
+          if (x >= a1) {
+            all = false;
+            continue;
+          }
+          if (doc_row[x] != uni) {
+            all = false;
+            continue;
+          }
+          // q rows see keys [q - left, q + right]; k columns are seen by rows [k - right, k + left]
+          int lo_b = b0, hi_b = b1;
+          const int below = q_side ? m.left : m.right, above = q_side ? m.right : m.left;
+          if (below >= 0) lo_b = max(lo_b, x - below);
+          if (above >= 0) hi_b = min(hi_b, x + above);
+          any |= lo_b <= hi_b;
+          all &= lo_b == b0 && hi_b == b1;
+        }
+        live = __any(any);
+        full = live && __all(all);
       } else {
-        // a block crosses a document boundary: every element (a padded tile
-        // element outside either sequence counts as masked)
+        // both blocks cross a document boundary: every element (a padded tile
+        // element outside either sequence counts as masked).  The key block's
+        // ids go to this wave's LDS row; each lane takes query rows and
+        // compares the keys inside the row's window.
+        int* kid = kd_lds[w];
+        for (int t = lane; t < ke - ka; t += 64) kid[t] = doc_row[ka + t];
+        __builtin_amdgcn_wave_barrier();
         bool any = false, all = complete;
         for (int r = lane; r < m.block; r += 64) {
           const int q = qa + r;
@@ -114,12 +153,17 @@ __global__ __launch_bounds__(256) void mb_classify(MaskBuild m) {
             continue;
           }
           const int dq = doc_row[q];
-          for (int k = ka; k < ke; ++k) {
-            const bool keep = mb_window(m, q, k) && dq == doc_row[k];
-            any |= keep;
-            all &= keep;
+          int k0 = ka, k1 = ke - 1;  // keys of the block inside q's window
+          if (m.left >= 0) k0 = max(k0, q - m.left);
+          if (m.right >= 0) k1 = min(k1, q + m.right);
+          if (k0 > ka || k1 < ke - 1) all = false;
+          for (int k = k0; k <= k1; ++k) {
+            const bool same = kid[k - ka] == dq;
+            any |= same;
+            all &= same;
           }
         }
+        __builtin_amdgcn_wave_barrier();
         live = __any(any);
         full = live && __all(all);
       }

@@ -99,7 +99,7 @@ def test_mask_build_workspace_layout():
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(abi_version=99), -8), (dict(q_len=0), -2), (dict(block=0), -2),
+    (dict(abi_version=99), -8), (dict(q_len=0), -2), (dict(block=0), -2), (dict(block=2048), -2),
     (dict(rows=2), -2),                                  # several table rows need document ids
     (dict(doc_ids=16, doc_len=999), -2),                 # ids shorter than the sequences
     (dict(q_len=64 * 65535, block=64), -2),              # too many blocks for one launch
