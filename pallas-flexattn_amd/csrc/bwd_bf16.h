@@ -360,6 +360,17 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   const int kw = k0 + 32 * w + lr;
   const bool kvalid = kw < P.Skv;
 
+  // The first tile's table entry is requested first of all (both lists'
+  // first entries; rows hold q_width >= 1 entries), ahead of the K / V rows
+  // and of the counts, so the first tile's copy waits for neither (valid when
+  // the first tile comes from the first head's lists).
+  const bool spec0 = P.has_tables && (P.tab_h == 1 || g == 1);
+  int first_full = 0, first_part = 0;
+  if (spec0) {
+    const int row = tab_row(P, b, hk * g, k0 / P.mblk_kv, P.n_kvblk);
+    if (P.full_q_num) first_full = vload_i32(P.full_q_idx + (size_t)row * P.q_width, 0, P.q_width);
+    if (P.q_num) first_part = vload_i32(P.q_idx + (size_t)row * P.q_width, 0, P.q_width);
+  }
   frag kf[KSTEPS], vf[KSTEPS];
   {
     const i32x4 rk = make_rsrc(static_cast<const char*>(a.k) + (size_t)head * P.Skv * RB, (uint32_t)P.Skv * RB);
@@ -370,11 +381,6 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
       vf[s] = buf_load16(rv, kw * RB + (2 * s + hh) * 16);
     }
   }
-  // V is kept negated (bf16 sign flips), so the dP MFMA accumulates -dP onto
-  // whatever its accumulator starts from: the fast path starts it from Delta
-  // and gets Delta - dP, dS = -P (Delta - dP) with one multiply per element.
-#pragma unroll
-  for (int s = 0; s < KSTEPS; ++s) vf[s] ^= 0x80008000u;
   int qlo, qhi;  // queries that see this lane's key (masks are intervals here)
   query_interval(P, b, kw, &qlo, &qhi);
 
@@ -621,7 +627,7 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   int hq_next = 0, qb_next = 0;
   TileRef ref_next{0, 0, 0};
   if (n_it > 0) {
-    const TileRef r0 = walk.fetch(0);
+    const TileRef r0 = spec0 ? TileRef{walk.count_full() > 0 ? first_full : first_part, 0, walk.hq0} : walk.fetch(0);
     hq_next = r0.hq;
     qb_next = walk.qbase(r0);
     issue(hq_next, qb_next, 0);
@@ -631,6 +637,14 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   // complete on every path into the loop
   wait_vmem();
   __syncthreads();
+  // V is kept negated (bf16 sign flips), so the dP MFMA accumulates -dP onto
+  // whatever its accumulator starts from: the fast path starts it from Delta
+  // and gets Delta - dP, dS = -P (Delta - dP) with one multiply per element.
+  // (Done here, after the prologue's wait, so the K / V loads overlap the
+  // table lookups and the first tile's copy.)
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int s = 0; s < KSTEPS; ++s) vf[s] ^= 0x80008000u;
   auto step = [&](int it, auto masked_c) {
     const int buf = it & 1;
     const int hq = hq_next, qbase = qb_next;
@@ -670,20 +684,14 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
     mfma_drain<'a'>(dka[i]);
     mfma_drain<'a'>(dva[i]);
   }
-  if (kvalid) {
-    uint16_t* dkp = static_cast<uint16_t*>(a.dk) + ((size_t)head * P.Skv + kw) * D;
-    uint16_t* dvp = static_cast<uint16_t*>(a.dv) + ((size_t)head * P.Skv + kw) * D;
-#pragma unroll
-    for (int i = 0; i < DT; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int d0 = 32 * i + 8 * j + 4 * hh;
-        *reinterpret_cast<u32x2*>(dkp + d0) =
-            u32x2{pack_bf16x2(dka[i][4 * j] * P.scale, dka[i][4 * j + 1] * P.scale),
-                  pack_bf16x2(dka[i][4 * j + 2] * P.scale, dka[i][4 * j + 3] * P.scale)};
-        *reinterpret_cast<u32x2*>(dvp + d0) = u32x2{pack_bf16x2(dva[i][4 * j], dva[i][4 * j + 1]),
-                                                    pack_bf16x2(dva[i][4 * j + 2], dva[i][4 * j + 3])};
-      }
+  // dK, dV rows of this wave, staged through the (now idle) tile buffers
+  {
+    const int rows_left = P.Skv - (k0 + 32 * w);
+    uint16_t* dkp = static_cast<uint16_t*>(a.dk) + ((size_t)head * P.Skv + k0 + 32 * w) * D;
+    uint16_t* dvp = static_cast<uint16_t*>(a.dv) + ((size_t)head * P.Skv + k0 + 32 * w) * D;
+    char* stage = lds + w * 2 * (32 * RB);
+    store_rows_bf16<D>(dka, P.scale, stage, dkp, rows_left, lane);
+    store_rows_bf16<D>(dva, 1.0f, stage + 32 * RB, dvp, rows_left, lane);
   }
 }
 

@@ -139,6 +139,40 @@ __device__ __forceinline__ void mfma_drain(f32x16& acc) {
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(acc));
 }
 
+// Store of a wave's 32-row accumulator block as bf16 rows of a row-major
+// (rows, D) tensor.  In the MFMA 32x32 layout lane l holds row (l & 31) and
+// element e of tile i holds column 32 i + acc_row(e, l >> 5): stored directly,
+// every instruction would write 8 bytes into each of 32 rows.  The block is
+// staged instead through `stage` (the wave's own 32 * 2D bytes of LDS, 16-byte
+// chunks swizzled by the row) and written back 16 bytes per lane with
+// consecutive lanes along a row, so each instruction writes whole row
+// segments.  `scale` multiplies lane l's row (per-row factors: the lane's
+// own value); rows at or past `rows_left` are not written.  The caller makes
+// sure no other wave uses `stage` meanwhile.
+template <int D>
+__device__ __forceinline__ void store_rows_bf16(const f32x16* acc, float scale, char* stage, uint16_t* rows,
+                                                int rows_left, int lane) {
+  constexpr int RB = 2 * D, NCH = D / 8, DT = D / 32;
+  constexpr int RPI = 64 / NCH;  // rows per store instruction
+  const int r = lane & 31, hh = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < DT; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = 4 * i + j;  // 16-byte chunk of columns 32 i + 8 j .. + 7
+      *reinterpret_cast<u32x2*>(stage + r * RB + ((c ^ (r % NCH)) * 16) + hh * 8) =
+          u32x2{pack_bf16x2(acc[i][4 * j] * scale, acc[i][4 * j + 1] * scale),
+                pack_bf16x2(acc[i][4 * j + 2] * scale, acc[i][4 * j + 3] * scale)};
+    }
+  const int c = lane % NCH;
+#pragma unroll
+  for (int k = 0; k < 32 / RPI; ++k) {
+    const int rr = k * RPI + lane / NCH;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(stage + rr * RB + ((c ^ (rr % NCH)) * 16));
+    if (rr < rows_left) *reinterpret_cast<u32x4*>(rows + (size_t)rr * D + c * 8) = v;
+  }
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
