@@ -317,18 +317,10 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
 
 #pragma unroll
   for (int i = 0; i < DT; ++i) mfma_drain<'v'>(dqa[i]);
-  if (qvalid) {
-    uint16_t* dqp = static_cast<uint16_t*>(a.dq) + rowi * D;
-#pragma unroll
-    for (int i = 0; i < DT; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int d0 = 32 * i + 8 * j + 4 * hh;
-        *reinterpret_cast<u32x2*>(dqp + d0) =
-            u32x2{pack_bf16x2(dqa[i][4 * j] * P.scale, dqa[i][4 * j + 1] * P.scale),
-                  pack_bf16x2(dqa[i][4 * j + 2] * P.scale, dqa[i][4 * j + 3] * P.scale)};
-      }
-  }
+  // dQ rows of this wave, staged through the (now idle) tile buffers
+  store_rows_bf16<D>(dqa, P.scale, lds + w * (32 * RB),
+                     static_cast<uint16_t*>(a.dq) + ((size_t)head * P.Sq + q0 + 32 * w) * D, P.Sq - (q0 + 32 * w),
+                     lane);
 }
 
 // ---------------------------------------------------------------- dK dV ----

@@ -307,19 +307,11 @@ void fwd_bf16_kernel(FwdArgs a) {
   for (int i = 0; i < DT; ++i) mfma_drain<FA_FWD_OREG>(oacc[i]);
   const float lt = pair_sum(l);
   const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-  if (qvalid) {
-    uint16_t* op = static_cast<uint16_t*>(a.o) + ((size_t)head * P.Sq + qw) * D;
-#pragma unroll
-    for (int i = 0; i < DT; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int d0 = 32 * i + 8 * j + 4 * hh;
-        *reinterpret_cast<u32x2*>(op + d0) =
-            u32x2{pack_bf16x2(oacc[i][4 * j] * inv, oacc[i][4 * j + 1] * inv),
-                  pack_bf16x2(oacc[i][4 * j + 2] * inv, oacc[i][4 * j + 3] * inv)};
-      }
-    if (hh == 0) a.lse[(size_t)head * P.Sq + qw] = lt > 0.f ? (m + log2f(lt)) * kLn2 : -INFINITY;
-  }
+  // O rows of this wave, staged through the (now idle) K / V buffers
+  store_rows_bf16<D>(oacc, inv, lds + w * (32 * RB),
+                     static_cast<uint16_t*>(a.o) + ((size_t)head * P.Sq + q0 + 32 * w) * D, P.Sq - (q0 + 32 * w),
+                     lane);
+  if (qvalid && hh == 0) a.lse[(size_t)head * P.Sq + qw] = lt > 0.f ? (m + log2f(lt)) * kLn2 : -INFINITY;
 }
 
 }  // namespace fa
