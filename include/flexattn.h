@@ -23,6 +23,8 @@
  *
  * Layouts: q, o, dq are (B, Hq, Sq, D) row-major; k, v, dk, dv are
  * (B, Hkv, Skv, D); lse is (B, Hq, Sq) float32 in natural-log units.
+ * The q, k, v, o, dout, dq, dk, dv pointers must be 16-byte aligned
+ * (FA_ERR_SHAPE otherwise): rows move 16 bytes per lane.
  * Grouped-query attention: q head h reads kv head h / (Hq / Hkv).
  */
 #ifndef FLEXATTN_H_

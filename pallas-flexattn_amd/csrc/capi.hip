@@ -2,6 +2,8 @@
 // kernel launches.  See include/flexattn.h for the contract.
 #include <hip/hip_runtime.h>
 
+#include <initializer_list>
+
 #include "../../include/flexattn.h"
 #include "bwd.h"
 #include "bwd_bf16.h"
@@ -124,6 +126,13 @@ int build_problem(const fa_params* p, const Tiles& t, Problem* pr) {
 }
 
 int launch_status() { return hipGetLastError() == hipSuccess ? FA_OK : FA_ERR_LAUNCH; }
+
+// Tensor rows are read and written 16 bytes per lane.
+bool aligned16(std::initializer_list<const void*> ptrs) {
+  for (const void* x : ptrs)
+    if (reinterpret_cast<uintptr_t>(x) & 15) return false;
+  return true;
+}
 
 // The bf16 LDS-DMA kernels evaluate masks as per-lane intervals (windows and
 // contiguous documents); arbitrary document labels go to the generic kernels.
@@ -296,6 +305,7 @@ int fa_fwd(const fa_params* p, const void* q, const void* k, const void* v, void
   rc = build_problem(p, t, &a.p);
   if (rc) return rc;
   if (!q || !k || !v || !o || !lse) return FA_ERR_NULL;
+  if (!aligned16({q, k, v, o})) return FA_ERR_SHAPE;
   if (a.p.has_tables && (a.p.mblk_q % t.bm || a.p.mblk_kv % t.bn)) return FA_ERR_TABLES;
   if (a.p.has_tables && !a.p.kv_num && !a.p.full_kv_num) return FA_ERR_TABLES;
   a.q = q;
@@ -320,6 +330,7 @@ int fa_bwd(const fa_params* p, const void* q, const void* k, const void* v, cons
            size_t workspace_bytes, void* stream) {
   if (!p) return FA_ERR_NULL;
   if (!q || !k || !v || !o || !lse || !dout || !dq || !dk || !dv) return FA_ERR_NULL;
+  if (!aligned16({q, k, v, o, dout, dq, dk, dv})) return FA_ERR_SHAPE;
   if (!workspace || workspace_bytes < delta_bytes(p)) return FA_ERR_WORKSPACE;
   BwdArgs a{};
   a.q = q;
@@ -338,6 +349,7 @@ int fa_bwd(const fa_params* p, const void* q, const void* k, const void* v, cons
 int fa_bwd_preprocess(const fa_params* p, const void* o, const void* dout, float* delta, void* stream) {
   if (!p) return FA_ERR_NULL;
   if (!o || !dout || !delta) return FA_ERR_NULL;
+  if (!aligned16({o, dout})) return FA_ERR_SHAPE;
   BwdArgs a{};
   a.o = o;
   a.dout = dout;
@@ -349,6 +361,7 @@ int fa_bwd_dkdv(const fa_params* p, const void* q, const void* k, const void* v,
                 const float* lse, const float* delta, void* dk, void* dv, void* stream) {
   if (!p) return FA_ERR_NULL;
   if (!q || !k || !v || !dout || !lse || !delta || !dk || !dv) return FA_ERR_NULL;
+  if (!aligned16({q, k, v, dout, dk, dv})) return FA_ERR_SHAPE;
   BwdArgs a{};
   a.q = q;
   a.k = k;
@@ -365,6 +378,7 @@ int fa_bwd_dq(const fa_params* p, const void* q, const void* k, const void* v, c
               const float* lse, const float* delta, void* dq, void* stream) {
   if (!p) return FA_ERR_NULL;
   if (!q || !k || !v || !dout || !lse || !delta || !dq) return FA_ERR_NULL;
+  if (!aligned16({q, k, v, dout, dq})) return FA_ERR_SHAPE;
   BwdArgs a{};
   a.q = q;
   a.k = k;

@@ -64,6 +64,15 @@ def test_fwd_rejects_bad_params_before_any_launch(kw, code):
     assert lib.fa_fwd(ctypes.byref(p), dummy, dummy, dummy, dummy, dummy, None) == code
 
 
+def test_misaligned_tensors_rejected():
+    lib = _lib.load()
+    p = _params()
+    ok, odd = ctypes.c_void_p(256), ctypes.c_void_p(264)
+    assert lib.fa_fwd(ctypes.byref(p), ok, ok, ok, odd, ok, None) == -2
+    assert lib.fa_bwd_dq(ctypes.byref(p), ok, ok, ok, ok, ok, ok, odd, None) == -2
+    assert lib.fa_bwd_dkdv(ctypes.byref(p), ok, odd, ok, ok, ok, ok, ok, ok, None) == -2
+
+
 def test_null_pointers_and_small_workspace_rejected():
     lib = _lib.load()
     p = _params()
