@@ -1,6 +1,6 @@
 """FlexAttention benchmark on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--config c2|c3|c4|c5|ns] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--config c2|c3|c4|c5|ns|decode] [--no-cpu]
 
 A step is one forward + backward pass (fa_fwd, fa_bwd_preprocess,
 fa_bwd_dkdv, fa_bwd_dq through the C ABI, outputs preallocated, inputs
@@ -144,6 +144,43 @@ def cpu_baseline(cfg, arrays, pairs_per_head, target_s):
                       f"{t:.1f} s; same unmasked-FLOP count as the GPU value"}
 
 
+def bench_decode(args):
+    """Decoding-shaped forward: one query per (batch, q head) against a long
+    KV cache, bf16, no mask (B8 Hq32 Hkv8 Skv32768 D128).  HBM-bound: the
+    metric is KV-cache bytes read per second, split-KV (flex_decode) next to
+    the unsplit forward (flex_attention)."""
+    import torch
+    import pallas_flexattn as pf
+    B, Hq, Hkv, Sq, Skv, D = 8, 32, 8, 1, 32768, 128
+    g = torch.Generator(device="cuda").manual_seed(6)
+    q = torch.randn(B, Hq, Sq, D, device="cuda", generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, Skv, D, device="cuda", generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, Skv, D, device="cuda", generator=g).to(torch.bfloat16)
+    stream = torch.cuda.current_stream()
+    split = lambda: pf.flex_decode(q, k, v, enable_gqa=True)
+    plain = lambda: pf.flex_attention(q, k, v, enable_gqa=True)
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 0.5:
+        split()
+        plain()
+        torch.cuda.synchronize()
+    ms_split = time_region(split, args.steps, stream)
+    ms_plain = time_region(plain, args.steps, stream)
+    kv_bytes = 2.0 * B * Hkv * Skv * D * 2
+    gbs = kv_bytes / (ms_split * 1e-3) / 1e9
+    out = {
+        "metric": "KV-cache read bandwidth, decode forward (split-KV)", "value": round(gbs, 1), "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "ms_per_step": round(ms_split, 4), "higher_is_better": True,
+        "dtype": "bf16", "data": "synthetic (torch normals rounded to bf16)",
+        "config": {"workload": "decode B8 Hq32 Hkv8 Sq1 Skv32768 D128 bf16, no mask", "B": B, "Hq": Hq, "Hkv": Hkv,
+                   "Sq": Sq, "Skv": Skv, "D": D},
+        "unsplit_forward_ms": round(ms_plain, 4),
+        "roofline": {"kernel": "fwd (split-KV) + merge", "bound": "hbm", "achieved": round(gbs, 1), "peak": 8000.0,
+                     "unit": "GB/s", "frac": round(gbs / 8000.0, 4), "traffic": None},
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -170,6 +207,10 @@ def main():
     import torch
     import pallas_flexattn as pf
     from pallas_flexattn.flash_attn import Runner
+
+    if args.config == "decode":
+        bench_decode(args)
+        return
 
     if args.profile_kernel == "copy":
         src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")

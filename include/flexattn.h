@@ -104,6 +104,19 @@ typedef struct fa_params {
 int fa_fwd(const fa_params *p, const void *q, const void *k, const void *v, void *o, float *lse,
            void *stream);
 
+/* Split-KV forward (decode and other short-query shapes): each (batch, head,
+ * query tile) walk is cut into n_splits key ranges computed by separate
+ * workgroups, whose partial results (unnormalised O, running maximum and sum,
+ * in the workspace) a second kernel merges into o and lse — the same outputs
+ * as fa_fwd.  n_splits <= 0 picks about two workgroups per CU with at least
+ * four key tiles per split; at most 64.  Only the bf16 interval-mask kernel
+ * splits; other problems run as fa_fwd (workspace unused).  No reference
+ * counterpart (decode is on the reference's roadmap); workspace of
+ * fa_fwd_splitkv_workspace_bytes(p, n_splits) bytes, 16-byte aligned. */
+size_t fa_fwd_splitkv_workspace_bytes(const fa_params *p, int n_splits);
+int fa_fwd_splitkv(const fa_params *p, const void *q, const void *k, const void *v, void *o, float *lse,
+                   int n_splits, void *workspace, size_t workspace_bytes, void *stream);
+
 /* Bytes of device scratch fa_bwd needs for these params. */
 size_t fa_bwd_workspace_bytes(const fa_params *p);
 

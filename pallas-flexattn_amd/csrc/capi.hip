@@ -144,11 +144,17 @@ int run_fwd(const FwdArgs& a, hipStream_t s) {
   const int grid = a.p.B * a.p.Hq * cdiv(a.p.Sq, 32 * NW);
   if constexpr (sizeof(T) == 2) {
     if (interval_masks(a.p)) {  // bf16: LDS-DMA + transposing-read kernel
-      hipLaunchKernelGGL((fa::fwd_bf16_kernel<D, BN, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
+      hipLaunchKernelGGL((fa::fwd_bf16_kernel<D, BN, NW, M>), dim3(grid * a.n_splits), dim3(NW * 64), 0, s, a);
+      if (a.n_splits > 1) {
+        const size_t n = (size_t)a.p.B * a.p.Hq * a.p.Sq * D;
+        hipLaunchKernelGGL((fa::fwd_split_merge<D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
+      }
       return launch_status();
     }
   }
-  hipLaunchKernelGGL((fa::fwd_kernel<T, D, BN, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
+  FwdArgs g = a;  // the generic kernel has no split-KV form
+  g.n_splits = 1;
+  hipLaunchKernelGGL((fa::fwd_kernel<T, D, BN, NW, M>), dim3(grid), dim3(NW * 64), 0, s, g);
   return launch_status();
 }
 
@@ -274,6 +280,36 @@ int mask_layout(const fa_mask_build* m, MaskLayout* L) {
   return FA_OK;
 }
 
+// compute units of the current device (cached per device)
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// Split-KV: the requested count (<= 0: about two workgroups per CU, at least
+// four key tiles per split), or 1 where the generic kernel runs.
+int choose_splits(const fa_params* p, const Tiles& t, const Problem& pr, int requested) {
+  if (p->dtype != FA_DTYPE_BF16 || !interval_masks(pr)) return 1;
+  const int items = p->B * p->Hq * cdiv(p->Sq, t.bm);
+  const int max_by_keys = cdiv(p->Skv, 4 * t.bn);
+  int n = requested;
+  if (n <= 0) n = cdiv(2 * device_cus(), items);
+  if (n > max_by_keys) n = max_by_keys;
+  if (n > 64) n = 64;
+  return n < 1 ? 1 : n;
+}
+
+size_t split_bytes(const fa_params* p, int n) {
+  return n > 1 ? (size_t)n * p->B * p->Hq * p->Sq * (p->D + 2) * sizeof(float) : 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -293,6 +329,46 @@ const char* fa_strerror(int status) {
     case FA_ERR_VERSION: return "fa_params.abi_version does not match the library";
     default: return "unknown status";
   }
+}
+
+size_t fa_fwd_splitkv_workspace_bytes(const fa_params* p, int n_splits) {
+  Tiles t;
+  Problem pr;
+  if (!p || default_tiles(p, &t) || build_problem(p, t, &pr)) return 0;
+  if (n_splits > 64) return 0;
+  return split_bytes(p, choose_splits(p, t, pr, n_splits));
+}
+
+int fa_fwd_splitkv(const fa_params* p, const void* q, const void* k, const void* v, void* o, float* lse,
+                   int n_splits, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!p) return FA_ERR_NULL;
+  if (n_splits > 64) return FA_ERR_SHAPE;
+  Tiles t;
+  int rc = default_tiles(p, &t);
+  if (rc) return rc;
+  FwdArgs a;
+  rc = build_problem(p, t, &a.p);
+  if (rc) return rc;
+  if (!q || !k || !v || !o || !lse) return FA_ERR_NULL;
+  if (!aligned16({q, k, v, o})) return FA_ERR_SHAPE;
+  if (a.p.has_tables && (a.p.mblk_q % t.bm || a.p.mblk_kv % t.bn)) return FA_ERR_TABLES;
+  if (a.p.has_tables && !a.p.kv_num && !a.p.full_kv_num) return FA_ERR_TABLES;
+  a.n_splits = choose_splits(p, t, a.p, n_splits);
+  if (a.n_splits > 1) {
+    if (!workspace || workspace_bytes < split_bytes(p, a.n_splits) || !aligned16({workspace}))
+      return FA_ERR_WORKSPACE;
+    a.part = static_cast<float*>(workspace);
+  }
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.lse = lse;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool m = has_mods(a.p);
+  if (p->dtype == FA_DTYPE_BF16)
+    return m ? fwd_d<uint16_t, 64, true>(a, p->D, t.bm, s) : fwd_d<uint16_t, 64, false>(a, p->D, t.bm, s);
+  return m ? fwd_d<float, 32, true>(a, p->D, t.bm, s) : fwd_d<float, 32, false>(a, p->D, t.bm, s);
 }
 
 int fa_fwd(const fa_params* p, const void* q, const void* k, const void* v, void* o, float* lse,

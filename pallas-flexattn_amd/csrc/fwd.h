@@ -25,6 +25,12 @@ struct FwdArgs {
   const void* v;
   void* o;
   float* lse;  // (B, Hq, Sq), natural-log units
+  // Split-KV (n_splits > 1, bf16 DMA kernel only): workgroup blockIdx.x takes
+  // split blockIdx.x / items of its item's walk and writes, instead of o and
+  // lse, its unnormalised partial O (relative to 2^m) and (m, l) to `part`:
+  // (n_splits, B*Hq*Sq, D) floats, then (n_splits, B*Hq*Sq, 2).
+  int n_splits = 1;
+  float* part = nullptr;
 };
 
 // A tile of a walk whose table entry may still be in flight: fetch() issues

@@ -59,8 +59,10 @@ void fwd_bf16_kernel(FwdArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 31, hh = lane >> 5;
   const int nqt = (P.Sq + BM - 1) / BM;
+  const int n_items = P.B * P.Hq * nqt;
+  const int split = a.n_splits > 1 ? (int)blockIdx.x / n_items : 0;
   int head, qt;
-  work_item(blockIdx.x, P.B * P.Hq, nqt, P.xcd_remap, P.head_group_q, false, &head, &qt);
+  work_item((int)blockIdx.x - split * n_items, P.B * P.Hq, nqt, P.xcd_remap, P.head_group_q, false, &head, &qt);
   const int b = head / P.Hq, h = head - b * P.Hq;
   const int hk = h / (P.Hq / P.Hkv);
   const int q0 = qt * BM;
@@ -204,27 +206,30 @@ void fwd_bf16_kernel(FwdArgs a) {
 
   // Table entries are fetched two tiles ahead, resolved one tile ahead; the
   // full tiles come first in the walk.
+  // With split-KV this workgroup takes tiles [it0, it1) of the walk.
   const int n_full = walk.count_full();
+  const int it0 = a.n_splits > 1 ? (int)((long long)n_it * split / a.n_splits) : 0;
+  const int it1 = a.n_splits > 1 ? (int)((long long)n_it * (split + 1) / a.n_splits) : n_it;
   int kb_next = 0;
   TileRef ref_next{0, 0, 0};
-  if (n_it > 0) {
-    kb_next = walk.kbase(walk.fetch(0));
-    issue(kb_next, 0);
-    if (n_it > 1) ref_next = walk.fetch(1);
+  if (it0 < it1) {
+    kb_next = walk.kbase(walk.fetch(it0));
+    issue(kb_next, it0 & 1);
+    if (it0 + 1 < it1) ref_next = walk.fetch(it0 + 1);
   }
   // unconditional, so the wait-count analysis sees the register loads above
   // complete on every path into the loop
   wait_vmem();
   __syncthreads();
-  for (int it = 0; it < n_it; ++it) {
+  for (int it = it0; it < it1; ++it) {
     const int buf = it & 1;
     const int kbase = kb_next;
     bool masked = it >= n_full;
-    if (it + 1 < n_it) {
+    if (it + 1 < it1) {
       kb_next = walk.kbase(ref_next);
       issue(kb_next, buf ^ 1);
     }
-    if (it + 2 < n_it) ref_next = walk.fetch(it + 2);
+    if (it + 2 < it1) ref_next = walk.fetch(it + 2);
     if (kbase < P.Skv) {  // workgroup-uniform
       masked = masked || (kbase + BN > P.Skv);
       const char* kl = lds + buf * TILE;
@@ -307,11 +312,58 @@ void fwd_bf16_kernel(FwdArgs a) {
   for (int i = 0; i < DT; ++i) mfma_drain<FA_FWD_OREG>(oacc[i]);
   const float lt = pair_sum(l);
   const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+  if (a.n_splits > 1) {  // partial O (relative to 2^m) and (m, l) for the merge
+    const size_t rows = (size_t)P.B * P.Hq * P.Sq;
+    const size_t row = (size_t)head * P.Sq + qw;
+    if (qvalid) {
+      float* po = a.part + ((size_t)split * rows + row) * D;
+#pragma unroll
+      for (int i = 0; i < DT; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          *reinterpret_cast<f32x4*>(po + 32 * i + 8 * j + 4 * hh) =
+              f32x4{oacc[i][4 * j], oacc[i][4 * j + 1], oacc[i][4 * j + 2], oacc[i][4 * j + 3]};
+      if (hh == 0) {
+        float* pml = a.part + (size_t)a.n_splits * rows * D + ((size_t)split * rows + row) * 2;
+        *reinterpret_cast<float2*>(pml) = make_float2(m, lt);
+      }
+    }
+    return;
+  }
   // O rows of this wave, staged through the (now idle) K / V buffers
   store_rows_bf16<D>(oacc, inv, lds + w * (32 * RB),
                      static_cast<uint16_t*>(a.o) + ((size_t)head * P.Sq + q0 + 32 * w) * D, P.Sq - (q0 + 32 * w),
                      lane);
   if (qvalid && hh == 0) a.lse[(size_t)head * P.Sq + qw] = lt > 0.f ? (m + log2f(lt)) * kLn2 : -INFINITY;
+}
+
+// Split-KV merge: one thread per (row, column) of O.  With the splits'
+// partials O_s (relative to 2^m_s) and sums l_s: M = max m_s, L = sum l_s
+// 2^(m_s - M), O = sum O_s 2^(m_s - M) / L, LSE = (M + log2 L) ln 2.
+template <int D>
+__global__ __launch_bounds__(256) void fwd_split_merge(FwdArgs a) {
+  const Problem& P = a.p;
+  const size_t rows = (size_t)P.B * P.Hq * P.Sq;
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t row = idx / D;
+  const int d = (int)(idx - row * D);
+  if (row >= rows) return;
+  const float* pml = a.part + (size_t)a.n_splits * rows * D;
+  float mm = -INFINITY;
+  for (int s = 0; s < a.n_splits; ++s) mm = fmaxf(mm, pml[((size_t)s * rows + row) * 2]);
+  float L = 0.f, O = 0.f;
+  if (mm != -INFINITY) {
+    for (int s = 0; s < a.n_splits; ++s) {
+      const float ms = pml[((size_t)s * rows + row) * 2];
+      const float c = ms == -INFINITY ? 0.f : fast_exp2(ms - mm);
+      L += pml[((size_t)s * rows + row) * 2 + 1] * c;
+      O += a.part[((size_t)s * rows + row) * D + d] * c;
+    }
+  }
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  const uint32_t ob = pack_bf16x2(O * inv, 0.f);
+  static_cast<uint16_t*>(a.o)[row * D + d] = (uint16_t)(ob & 0xffffu);
+  if (d == 0) a.lse[row] = L > 0.f ? (mm + log2f(L)) * kLn2 : -INFINITY;
 }
 
 }  // namespace fa

@@ -8,6 +8,7 @@ from pallas_flexattn.flash_attn import (
     flash_attention_bwd,
     mha_reference,
     flex_attention,
+    flex_decode,
     flash_attention_bwd_preprocess,
     flash_attention_bwd_dkv,
     flash_attention_bwd_dq,
@@ -60,6 +61,7 @@ __all__ = [
     "print_kernel_config",
     # MI355X FlexAttention surface
     "flex_attention",
+    "flex_decode",
     "flash_attention_bwd_preprocess",
     "flash_attention_bwd_dkv",
     "flash_attention_bwd_dq",

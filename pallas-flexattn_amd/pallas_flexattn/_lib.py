@@ -56,7 +56,7 @@ class FaMaskBuild(ctypes.Structure):
     ]
 
 
-EXPORTED = ("fa_fwd", "fa_bwd", "fa_bwd_workspace_bytes", "fa_bwd_preprocess", "fa_bwd_dkdv", "fa_bwd_dq",
+EXPORTED = ("fa_fwd", "fa_fwd_splitkv", "fa_fwd_splitkv_workspace_bytes", "fa_bwd", "fa_bwd_workspace_bytes", "fa_bwd_preprocess", "fa_bwd_dkdv", "fa_bwd_dq",
             "fa_mask_build_workspace_bytes", "fa_build_block_mask", "fa_strerror", "fa_abi_version")
 
 _lib = None
@@ -80,6 +80,10 @@ def load():
     v = ctypes.c_void_p
     lib.fa_fwd.argtypes = [P, v, v, v, v, v, v]
     lib.fa_fwd.restype = ctypes.c_int
+    lib.fa_fwd_splitkv.argtypes = [P, v, v, v, v, v, ctypes.c_int, v, ctypes.c_size_t, v]
+    lib.fa_fwd_splitkv.restype = ctypes.c_int
+    lib.fa_fwd_splitkv_workspace_bytes.argtypes = [P, ctypes.c_int]
+    lib.fa_fwd_splitkv_workspace_bytes.restype = ctypes.c_size_t
     lib.fa_bwd.argtypes = [P, v, v, v, v, v, v, v, v, v, v, ctypes.c_size_t, v]
     lib.fa_bwd.restype = ctypes.c_int
     lib.fa_bwd_preprocess.argtypes = [P, v, v, v, v]

@@ -444,6 +444,38 @@ def flash_attention(q, k, v, mask_mod: Optional[MaskMod] = None, block_r: int = 
     return o
 
 
+def flex_decode(query, key, value, score_mod: Optional[ScoreSpec] = None, block_mask: Optional[BlockMask] = None,
+                scale: Optional[float] = None, enable_gqa: bool = False, num_splits: Optional[int] = None,
+                return_lse: bool = False):
+    """Forward-only FlexAttention for short query blocks against long key
+    sequences (decoding): the keys of each query tile are split into
+    ``num_splits`` ranges computed by separate workgroups and merged by their
+    log-sum-exp (C ABI ``fa_fwd_splitkv``; ``None`` picks about two workgroups
+    per CU).  Same results as :func:`flex_attention`'s forward; no gradient.
+    The reference has no decode kernel (it is on its roadmap)."""
+    torch = _torch()
+    if query.shape[1] != key.shape[1] and not enable_gqa:
+        raise ValueError("query and key head counts differ: pass enable_gqa=True for grouped-query attention")
+    mask = None
+    if block_mask is not None:
+        mask = _as_mask_spec(block_mask.mask_mod) if block_mask.mask_mod is not None else None
+        if not block_mask.has_tables:
+            raise ValueError("block_mask has no kernel tables (build it with create_block_mask)")
+    q, k, v = _dense16(query), _dense16(key), _dense16(value)
+    _check_inputs(q, k, v)
+    _, dname = _dtype_code(q)
+    plan = _Plan(q, k, mask, _as_score_spec(score_mod), scale, block_mask, (128, 64 if dname == "bf16" else 32))
+    o = torch.empty_like(q)
+    lse = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
+    lib = _lib.load()
+    n = 0 if num_splits is None else int(num_splits)
+    ws_bytes = lib.fa_fwd_splitkv_workspace_bytes(plan.ptr(), n)
+    ws = torch.empty(max(ws_bytes, 256), device=q.device, dtype=torch.uint8)
+    _lib.check(lib.fa_fwd_splitkv(plan.ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                  lse.data_ptr(), n, ws.data_ptr(), ws_bytes, _stream()))
+    return (o, lse) if return_lse else o
+
+
 def flex_attention(query, key, value, score_mod: Optional[ScoreSpec] = None,
                    block_mask: Optional[BlockMask] = None, scale: Optional[float] = None,
                    enable_gqa: bool = False, return_lse: bool = False, kernel_options: Optional[dict] = None):
