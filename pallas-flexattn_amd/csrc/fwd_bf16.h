@@ -9,10 +9,10 @@
 //     issued one tile ahead; block-table entries come through the scalar cache;
 //   * S^T = K Q^T   (A = K rows from LDS in perm23 order, fetched one k-step
 //     ahead of the MFMAs; B = Q from VGPRs);
-//   * online softmax with one query per lane: row max / sum are per-lane
-//     scalars plus a v_permlane32_swap between lane halves; the reference
-//     maximum may trail the running one by up to 2^8 in P, so O is rescaled
-//     only when some row maximum outgrows that; the scale is folded into the
+//   * online softmax with one query per lane, speculative: exponentials
+//     against the current reference maximum, no per-tile maximum; only a lane
+//     whose tile sum leaves [0, 2^16] sends the wave through the exact
+//     maximum / rescale (see softmax below); the scale is folded into the
 //     exponent's FMA; fully-live tiles skip the element mask, partial tiles
 //     keep keys in [lo, hi] (window and contiguous documents are intervals
 //     per query);
@@ -157,50 +157,72 @@ void fwd_bf16_kernel(FwdArgs a) {
     for (int e = 0; e < 16; ++e) oacc[i][e] = 0.f;
 #pragma unroll
   for (int i = 0; i < DT; ++i) mfma_drain<FA_FWD_OREG>(oacc[i]);
-  // Reference maximum m (log2 units, per row) and partial sum l.  m may trail
-  // the running maximum by up to kSlack: P = exp2(t - m) then stays below
-  // 2^kSlack, and O, l are rescaled only when a row maximum outgrows it (the
-  // normalisation O / l does not depend on which reference is used).
-  constexpr float kSlack = 8.0f;
+  // Reference maximum m (log2 units, per row) and partial sum l.  The
+  // exponentials of a tile are taken speculatively against the current m,
+  // with no maximum over the tile: P = exp2(t - m) goes straight into the
+  // bf16 fragments of the PV product and its float32 row sum into l (the
+  // unrounded P, as the reference sums it before the bf16 cast of PV).
+  // As long as a lane's sum over the tile stays within kSpill = 2^16
+  // (no P above 2^16: bf16 keeps its relative precision and the fp32 O and l
+  // stay far from overflow), the tile is done.  Otherwise (a row maximum grew
+  // by more than 16 in log2 units, a row's first live tile, or inf / NaN) the
+  // whole wave takes the exact path: row maximum, O and l rescaled to it, and
+  // the exponentials recomputed.  The normalisation O / l does not depend on
+  // which reference is used.
+  constexpr float kSpill = 65536.0f;
   float m = -INFINITY, l = 0.f;
 
-  // Online softmax of one tile held in sacc.  Without score mods sacc keeps
-  // raw q.k: the max is taken on it (scale > 0) and the scale is folded into
-  // the exponent's FMA.  With mods sacc holds log2-domain logits.
-  auto softmax = [&](f32x16* sacc) {
-    float mx = -INFINITY;
+  // Exponentials of a whole tile against reference muse, into the bf16
+  // fragments pf; returns the lane's float32 sum.  Without score mods sacc
+  // keeps raw (masked) q.k: the max is taken on it (scale > 0) and the scale
+  // is folded into the exponent's FMA.  With mods sacc holds log2-domain
+  // logits.
+  auto exps = [&](const f32x16* sacc, frag* pf, float muse) {
+    float rs0 = 0.f, rs1 = 0.f;
 #pragma unroll
-    for (int j = 0; j < NSUB; ++j)
+    for (int c = 0; c < BN / 16; ++c) {
+      float x[8];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sacc[j][e]);
-    float mt = pair_max(mx);
-    if constexpr (!kMods) mt *= P.scale_log2;
-    const float mnew = fmaxf(m, mt);
-    if (__any(mnew > m + kSlack)) {
-      const float alpha = fast_exp2(m - (mnew == -INFINITY ? 0.f : mnew));
-      l *= alpha;
-#pragma unroll
-      for (int i = 0; i < DT; ++i) mfma_drain<FA_FWD_OREG>(oacc[i]);
-#pragma unroll
-      for (int i = 0; i < DT; ++i)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) oacc[i][e] *= alpha;
-#pragma unroll
-      for (int i = 0; i < DT; ++i) mfma_drain<FA_FWD_OREG>(oacc[i]);
-      m = mnew;
-    }
-    const float muse = m == -INFINITY ? 0.f : m;
-    float rs = 0.f;
-#pragma unroll
-    for (int j = 0; j < NSUB; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        float pv;
-        if constexpr (kMods) pv = fast_exp2(sacc[j][e] - muse);
-        else pv = fast_exp2(fmaf(sacc[j][e], P.scale_log2, -muse));
-        sacc[j][e] = pv;
-        rs += pv;
+      for (int t = 0; t < 8; ++t) {
+        const float s = sacc[c >> 1][8 * (c & 1) + t];
+        if constexpr (kMods) x[t] = fast_exp2(s - muse);
+        else x[t] = fast_exp2(fmaf(s, P.scale_log2, -muse));
       }
+      pf[c] = E::pack(x);
+#pragma unroll
+      for (int t = 0; t < 8; t += 2) {
+        rs0 += x[t];
+        rs1 += x[t + 1];
+      }
+    }
+    return rs0 + rs1;
+  };
+  auto softmax = [&](const f32x16* sacc, frag* pf) {
+    float rs = exps(sacc, pf, m == -INFINITY ? 0.f : m);
+    if (__any(!(rs <= kSpill) || m == -INFINITY)) {  // exact path (wave-uniform)
+      float mx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < NSUB; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sacc[j][e]);
+      float mt = pair_max(mx);
+      if constexpr (!kMods) mt *= P.scale_log2;
+      const float mnew = fmaxf(m, mt);
+      if (__any(mnew > m)) {
+        const float alpha = fast_exp2(m - (mnew == -INFINITY ? 0.f : mnew));
+        l *= alpha;
+#pragma unroll
+        for (int i = 0; i < DT; ++i) mfma_drain<FA_FWD_OREG>(oacc[i]);
+#pragma unroll
+        for (int i = 0; i < DT; ++i)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) oacc[i][e] *= alpha;
+#pragma unroll
+        for (int i = 0; i < DT; ++i) mfma_drain<FA_FWD_OREG>(oacc[i]);
+        m = mnew;
+      }
+      rs = exps(sacc, pf, m == -INFINITY ? 0.f : m);
+    }
     l += rs;
   };
 
@@ -240,19 +262,25 @@ void fwd_bf16_kernel(FwdArgs a) {
       for (int j = 0; j < NSUB; ++j)
 #pragma unroll
         for (int e = 0; e < 16; ++e) sacc[j][e] = 0.f;
-      frag ka[2][NSUB];
+      // K fragments KPF k-steps ahead of their MFMAs (ds_read_b128 latency
+      // exceeds one step of two MFMAs)
+      constexpr int KPF = 2, KR = KPF + 1;
+      frag ka[KR][NSUB];
       if (FA_FWD_PRIO) __builtin_amdgcn_s_setprio(1);  // MFMA phase first in issue order
 #pragma unroll
-      for (int j = 0; j < NSUB; ++j) ka[0][j] = *reinterpret_cast<const u32x4*>(kl + j * 32 * RB + koffA[0]);
+      for (int s = 0; s < KPF; ++s)
+#pragma unroll
+        for (int j = 0; j < NSUB; ++j) ka[s][j] = *reinterpret_cast<const u32x4*>(kl + j * 32 * RB + koffA[s]);
 #pragma unroll
       for (int s = 0; s < KSTEPS; ++s) {
-        if (s + 1 < KSTEPS) {
+        if (s + KPF < KSTEPS) {
 #pragma unroll
           for (int j = 0; j < NSUB; ++j)
-            ka[(s + 1) & 1][j] = *reinterpret_cast<const u32x4*>(kl + j * 32 * RB + koffA[s + 1]);
+            ka[(s + KPF) % KR][j] = *reinterpret_cast<const u32x4*>(kl + j * 32 * RB + koffA[s + KPF]);
         }
 #pragma unroll
-        for (int j = 0; j < NSUB; ++j) sacc[j] = E::mma(ka[s & 1][j], qf[s], sacc[j]);
+        for (int j = 0; j < NSUB; ++j) sacc[j] = E::mma(ka[s % KR][j], qf[s], sacc[j]);
+        __builtin_amdgcn_sched_barrier(0);
       }
       if (FA_FWD_PRIO) __builtin_amdgcn_s_setprio(0);
 
@@ -275,16 +303,20 @@ void fwd_bf16_kernel(FwdArgs a) {
             sacc[j][e] = (key >= klo && key <= khi) ? sacc[j][e] : -INFINITY;
           }
       }
-      softmax(sacc);
-
+      // V^T fragments of d tile i (two tiles in flight): tile 0's reads issue
+      // before the softmax, tile i + 1's before tile i's MFMAs
+      frag vt[2][BN / 16];
+      auto load_vt = [&](int i) {
+#pragma unroll
+        for (int c = 0; c < BN / 16; ++c) {
+          const uint2 lo = lds_read_tr16(vl + voffT[i] + (16 * c) * RB);
+          const uint2 hi = lds_read_tr16(vl + voffT[i] + (16 * c + 4) * RB);
+          vt[i & 1][c] = u32x4{lo.x, lo.y, hi.x, hi.y};
+        }
+      };
+      load_vt(0);
       frag pf[BN / 16];
-#pragma unroll
-      for (int c = 0; c < BN / 16; ++c) {
-        float x[8];
-#pragma unroll
-        for (int t = 0; t < 8; ++t) x[t] = sacc[c >> 1][8 * (c & 1) + t];
-        pf[c] = E::pack(x);
-      }
+      softmax(sacc, pf);
       // the 2 wait states an MFMA needs after a VALU write of its operand,
       // once for all of P (the PV MFMAs then carry no s_nop)
       static_assert(BN / 16 == 4 || BN / 16 == 2, "P fragments");
@@ -293,15 +325,14 @@ void fwd_bf16_kernel(FwdArgs a) {
       else
         asm volatile("s_nop 1" : "+v"(pf[0]), "+v"(pf[1]));
       if (FA_FWD_PRIO) __builtin_amdgcn_s_setprio(1);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 0; i < DT; ++i)
+      for (int i = 0; i < DT; ++i) {
+        if (i + 1 < DT) load_vt(i + 1);
 #pragma unroll
-        for (int c = 0; c < BN / 16; ++c) {
-          const uint2 lo = lds_read_tr16(vl + voffT[i] + (16 * c) * RB);
-          const uint2 hi = lds_read_tr16(vl + voffT[i] + (16 * c + 4) * RB);
-          const frag vf = u32x4{lo.x, lo.y, hi.x, hi.y};
-          mfma_acc<FA_FWD_OREG, false>(oacc[i], vf, pf[c]);
-        }
+        for (int c = 0; c < BN / 16; ++c) mfma_acc<FA_FWD_OREG, false>(oacc[i], vt[i & 1][c], pf[c]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
       if (FA_FWD_PRIO) __builtin_amdgcn_s_setprio(0);
     }
     wait_vmem();

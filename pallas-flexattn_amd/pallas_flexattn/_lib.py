@@ -7,7 +7,9 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libflexattn.so")
+# FLEXATTN_LIB names another build of the same library (same ABI), e.g. to
+# time two builds side by side in one process tree.
+LIB_PATH = os.environ.get("FLEXATTN_LIB") or os.path.join(_HERE, "libflexattn.so")
 ABI_VERSION = 1
 
 DTYPE_BF16 = 0
