@@ -154,12 +154,8 @@ def tuned_tiles(seq_len: int, head_dim: int, dtype: str, sparse: bool) -> Option
     return (e["block_m"], e["block_n"]) if e else None
 
 
-def tune(batch: int = 4, heads: int = 32, seq_len: int = 4096, head_dim: int = 128, causal: bool = True,
-         dtype: str = "bf16", iters: int = 10, path: str = TUNE_TABLE) -> Dict[str, int]:
-    """Time every instantiated BLOCK_M for this shape on the current GPU
-    (fwd + bwd with hipEvents) and record the fastest in the JSON table."""
+def _tune_inputs(batch, heads, seq_len, head_dim, causal, dtype):
     import torch
-    from .flash_attn import flex_attention
     from .block_mask import create_block_mask
     from .mask_mod import causal_mask, bidirectional_mask
     dt = torch.bfloat16 if dtype == "bf16" else torch.float32
@@ -167,28 +163,80 @@ def tune(batch: int = 4, heads: int = 32, seq_len: int = 4096, head_dim: int = 1
     g = torch.Generator(device=dev).manual_seed(0)
     q, k, v, do = (torch.randn(batch, heads, seq_len, head_dim, device=dev, dtype=dt, generator=g) for _ in range(4))
     bm_mask = create_block_mask(causal_mask if causal else bidirectional_mask, 1, 1, seq_len, seq_len, 128)
+    return q, k, v, do, bm_mask
+
+
+def run_candidate(block_m: int, block_n: int = 64, batch: int = 4, heads: int = 32, seq_len: int = 4096,
+                  head_dim: int = 128, causal: bool = True, dtype: str = "bf16", iters: int = 3,
+                  backward: bool = False) -> None:
+    """Run one tile candidate ``iters`` times (forward, or forward + backward)
+    and nothing else: the program rocprofv3 counter passes are taken over
+    (MFMA busy cycles, HBM bytes) to compare candidates."""
+    import torch
+    from .flash_attn import flex_attention
+    q, k, v, do, bm_mask = _tune_inputs(batch, heads, seq_len, head_dim, causal, dtype)
+    opts = {"BLOCK_M": block_m, "BLOCK_N": block_n}
+    qq, kk, vv = (t.detach().requires_grad_(backward) for t in (q, k, v))
+    for _ in range(iters):
+        o = flex_attention(qq, kk, vv, block_mask=bm_mask, kernel_options=opts)
+        if backward:
+            o.backward(do)
+    torch.cuda.synchronize()
+
+
+def tune(batch: int = 4, heads: int = 32, seq_len: int = 4096, head_dim: int = 128, causal: bool = True,
+         dtype: str = "bf16", iters: int = 10, path: str = TUNE_TABLE) -> Dict[str, int]:
+    """Time every instantiated (BLOCK_M, BLOCK_N) for this shape on the current
+    GPU with hipEvents -- BLOCK_M = 32 x the waves per workgroup (2 or 4), each
+    wave owning 32 query rows; the K / V tiles are double-buffered in LDS in
+    every candidate -- and record the fastest fwd + bwd in the JSON table,
+    with each candidate's forward and fwd + bwd time and TFLOP/s on the
+    unmasked pairs (fwd 4 D P, fwd + bwd 14 D P per head)."""
+    import torch
+    from .flash_attn import flex_attention
+    q, k, v, do, bm_mask = _tune_inputs(batch, heads, seq_len, head_dim, causal, dtype)
+    pairs = seq_len * (seq_len + 1) / 2 if causal else float(seq_len) * seq_len
+    flops_fwd = 4.0 * head_dim * pairs * batch * heads
+    peak = 2516.6 if dtype == "bf16" else 157.3
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(iters):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / iters
+
     results = {}
     for bm in SUPPORTED_BLOCK_M:
         for bn in SUPPORTED_BLOCK_N[dtype]:
             opts = {"BLOCK_M": bm, "BLOCK_N": bn}
             qq, kk, vv = (t.detach().requires_grad_() for t in (q, k, v))
-            for _ in range(2):
+
+            def fwd_only():
+                with torch.no_grad():
+                    flex_attention(q, k, v, block_mask=bm_mask, kernel_options=opts)
+
+            def fwd_bwd():
                 o = flex_attention(qq, kk, vv, block_mask=bm_mask, kernel_options=opts)
                 o.backward(do)
-            torch.cuda.synchronize()
-            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s.record()
-            for _ in range(iters):
-                o = flex_attention(qq, kk, vv, block_mask=bm_mask, kernel_options=opts)
-                o.backward(do)
-            e.record()
-            torch.cuda.synchronize()
-            results[(bm, bn)] = s.elapsed_time(e) / iters
-    (bm, bn), ms = min(results.items(), key=lambda kv: kv[1])
+
+            t_f, t_fb = timed(fwd_only), timed(fwd_bwd)
+            results[(bm, bn)] = {"waves": bm // 32, "lds_buffers": 2, "ms_fwd": round(t_f, 4),
+                                 "ms_fwd_bwd": round(t_fb, 4),
+                                 "tflops_fwd": round(flops_fwd / t_f / 1e9, 1),
+                                 "tflops_fwd_bwd": round(3.5 * flops_fwd / t_fb / 1e9, 1),
+                                 "pct_peak_fwd_bwd": round(100 * 3.5 * flops_fwd / t_fb / 1e9 / peak, 2)}
+    (bm, bn), best = min(results.items(), key=lambda kv: kv[1]["ms_fwd_bwd"])
     table = load_tune_table(path)
     key = f"{dtype}/D{head_dim}/S{seq_len}/{'sparse' if causal else 'dense'}"
-    table[key] = {"block_m": bm, "block_n": bn, "ms_fwd_bwd": ms,
-                  "candidates": {f"{a}x{b}": t for (a, b), t in results.items()}}
+    table[key] = {"block_m": bm, "block_n": bn, "ms_fwd_bwd": best["ms_fwd_bwd"],
+                  "shape": f"B{batch} H{heads} S{seq_len} D{head_dim} {'causal' if causal else 'dense'}",
+                  "candidates": {f"{a}x{b}": r for (a, b), r in results.items()}}
     with open(path, "w") as f:
         json.dump(table, f, indent=1, sort_keys=True)
     return table[key]
@@ -205,8 +253,15 @@ if __name__ == "__main__":
     parser.add_argument("--mask-type", type=str, default=None,
                         choices=['causal', 'sliding_window', 'bidirectional'])
     parser.add_argument("--tune", action="store_true", help="measure tiles on this GPU and record them")
+    parser.add_argument("--run-candidate", type=int, default=None, metavar="BLOCK_M",
+                        help="only run this BLOCK_M (for rocprofv3 counter passes)")
+    parser.add_argument("--backward", action="store_true", help="--run-candidate: forward + backward")
+    parser.add_argument("--iters", type=int, default=3)
     args = parser.parse_args()
-    if args.tune:
+    if args.run_candidate is not None:
+        run_candidate(args.run_candidate, 64, args.batch_size, args.num_heads, args.seq_len, args.head_dim,
+                      args.mask_type == "causal", iters=args.iters, backward=args.backward)
+    elif args.tune:
         print(tune(args.batch_size, args.num_heads, args.seq_len, args.head_dim, args.mask_type == "causal"))
     else:
         print_kernel_config(args.batch_size, args.num_heads, args.seq_len, args.head_dim, args.mask_type)

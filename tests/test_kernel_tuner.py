@@ -54,3 +54,21 @@ def test_kernel_tile_mapping():
     assert kernel_tiles(128, 128, "fp32") == (128, 32)
     for br in (32, 64, 128, 256):
         assert kernel_tiles(br, 64, "bf16")[0] in SUPPORTED_BLOCK_M
+
+
+def test_committed_tune_table_is_consistent():
+    """The measured table shipped with the package: every entry names an
+    instantiated tile pair and is the fastest fwd + bwd of its candidates."""
+    from pallas_flexattn.kernel_tuner import SUPPORTED_BLOCK_N, load_tune_table, TUNE_TABLE
+    import os
+    if not os.path.exists(TUNE_TABLE):
+        pytest.skip("no tune table")
+    table = load_tune_table()
+    assert table
+    for key, e in table.items():
+        dtype = key.split("/")[0]
+        assert e["block_m"] in SUPPORTED_BLOCK_M and e["block_n"] in SUPPORTED_BLOCK_N[dtype]
+        best = min(e["candidates"].items(), key=lambda kv: kv[1]["ms_fwd_bwd"])[0]
+        assert best == f"{e['block_m']}x{e['block_n']}"
+        for c in e["candidates"].values():
+            assert c["waves"] * 32 in SUPPORTED_BLOCK_M and c["ms_fwd"] < c["ms_fwd_bwd"]
