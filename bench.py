@@ -1,7 +1,11 @@
 """FlexAttention benchmark on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--config c2|c3|c4|c5|ns|decode] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--config ns|c2|c3|c4|c5|decode] [--others c2,c3,c4,c5] [--no-cpu]
 
+The headline workload (default ns) is causal attention B4 H32 S8192 D128 in
+bf16, the shape the 50 % / 35 % targets are set on; the other workloads
+(C2 causal S2048, C3 sliding window, C4 GQA + ALiBi + soft-cap, C5 packed
+documents) are timed after it and reported as extra keys.
 A step is one forward + backward pass (fa_fwd, fa_bwd_preprocess,
 fa_bwd_dkdv, fa_bwd_dq through the C ABI, outputs preallocated, inputs
 resident in HBM) over one batch of synthetic inputs.  Throughput counts only
@@ -9,10 +13,13 @@ unmasked (query, key) pairs P per (batch, head): fwd 4*D*P, bwd 10*D*P,
 fwd+bwd 14*D*P FLOPs (recomputation is not credited).
 
 Prints ONE JSON line.  ``value`` is the fwd+bwd effective TFLOP/s; the line
-also carries the forward figure, per-kernel times, the roofline of the
-dominant kernel (HIP events on the launch stream) and the CPU baseline: the
-oracle's C restatement of the reference's tiled algorithm, timed on a bounded
-sample of heads of the same workload on this host.
+also carries the forward figure, per-kernel times, the public
+``flex_attention`` forward + autograd backward time on the same inputs, the
+roofline of the dominant kernel (HIP events on the launch stream; HBM bytes
+per launch from profiles/traffic.json only when that file was measured on the
+current kernel sources) and the CPU baseline: the oracle's C restatement of
+the reference's tiled algorithm, timed on a bounded sample of heads of the
+same workload on this host.
 """
 import argparse
 import json
@@ -181,6 +188,73 @@ def bench_decode(args):
     print(json.dumps(out), flush=True)
 
 
+def sources_sha256():
+    """Hash of the HIP sources and the C ABI header: identifies the kernels a
+    counter measurement was taken on."""
+    import hashlib
+    h = hashlib.sha256()
+    csrc = os.path.join(ROOT, "pallas-flexattn_amd", "csrc")
+    for name in sorted(os.listdir(csrc)):
+        if name.endswith((".h", ".hip")):
+            with open(os.path.join(csrc, name), "rb") as f:
+                h.update(name.encode() + b"\0" + f.read())
+    with open(os.path.join(ROOT, "include", "flexattn.h"), "rb") as f:
+        h.update(f.read())
+    return h.hexdigest()
+
+
+def measured_traffic(config, kernel):
+    """HBM bytes per launch of `kernel` at `config` from profiles/traffic.json,
+    only if it was measured on the current kernel sources (else None)."""
+    tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(tpath):
+        return None
+    with open(tpath) as f:
+        table = json.load(f)
+    if table.get("sources_sha256") != sources_sha256():
+        return None
+    return table.get(f"{config}/{kernel}")
+
+
+def warm(fn, min_steps=3, min_s=0.5):
+    """Untimed steps until the GPU clock has settled (at least min_steps and
+    min_s seconds); returns the count."""
+    import torch
+    n, t0 = 0, time.perf_counter()
+    while n < min_steps or time.perf_counter() - t0 < min_s:
+        fn()
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return n
+
+
+def setup(name, dev, numpy_inputs):
+    """Inputs (bf16 on the GPU), the device-built block mask and a Runner for a
+    workload.  numpy_inputs: seeded numpy normals (as the CPU baseline uses);
+    otherwise torch normals drawn on the GPU with the same seed (same
+    distribution, no host round trip)."""
+    import torch
+    import pallas_flexattn as pf
+    from pallas_flexattn.flash_attn import Runner
+    cfg = make_config(name)
+    B, Hq, Hkv, S, D = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["S"], cfg["D"]
+    arrays = None
+    if numpy_inputs:
+        arrays = gen_inputs(cfg)
+        tq, tk, tv, tdo = (torch.from_numpy(a).to(dev, torch.bfloat16) for a in arrays)
+    else:
+        g = torch.Generator(device=dev).manual_seed(cfg["seed"])
+        sc = cfg["scale_in"]
+        tq, tk, tv = ((torch.randn(B, h, S, D, device=dev, generator=g) * sc).to(torch.bfloat16)
+                      for h in (Hq, Hkv, Hkv))
+        tdo = torch.randn(B, Hq, S, D, device=dev, generator=g).to(torch.bfloat16)
+    bmask = pf.create_block_mask(cfg["mask"], B, Hq, S, S, 128, device=dev)
+    runner = Runner(tq, tk, tv, tdo, score_mod=cfg["score"], block_mask=bmask)
+    return cfg, arrays, (tq, tk, tv, tdo), bmask, runner
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -188,7 +262,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=None,
                     help="untimed warm-up steps (default: at least 3 steps and 0.5 s, so the GPU clock has "
                          "settled before the timed steps; the count used is reported)")
-    ap.add_argument("--config", default="c2")
+    ap.add_argument("--config", default="ns",
+                    help="headline workload: ns (causal B4 H32 S8192 D128, default), c2, c3, c4, c5, decode")
+    ap.add_argument("--others", default="c2,c3,c4,c5",
+                    help="further workloads reported as extra keys (fwd and fwd+bwd TFLOP/s); '' for none")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--profile-kernel", choices=("fwd", "dkdv", "dq", "copy"), default=None,
@@ -196,8 +273,8 @@ def main():
                          "copy = a 256 MiB device copy used to calibrate FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--profile-iters", type=int, default=3)
     ap.add_argument("--dense-ref", action="store_true",
-                    help="also time the same shape with no mask (every tile live) and report the time fraction "
-                         "next to the live-block fraction (sparse-proportionality check)")
+                    help="also time the headline shape with no mask (every tile live) and report the time "
+                         "fraction next to the live-block fraction (sparse-proportionality check)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported (run with --gpus 1)",
@@ -221,33 +298,14 @@ def main():
         log(f"profile: {args.profile_iters} copies of 256 MiB")
         return
 
-    cfg = make_config(args.config)
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    cfg, arrays, (tq, tk, tv, tdo), bmask, runner = setup(args.config, dev, numpy_inputs=not args.no_cpu)
     B, Hq, Hkv, S, D = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["S"], cfg["D"]
     log(f"config {args.config}: {cfg['workload']}")
-    arrays = gen_inputs(cfg)
-    dev = torch.device("cuda:0")
-    tq, tk, tv, tdo = (torch.from_numpy(a).to(dev, torch.bfloat16) for a in arrays)
-    # block mask: built on the GPU (timed over 5 builds after a first one,
-    # each ending in the copy of the tables to the host), and on the host
-    t0 = time.perf_counter()
-    host_bmask = pf.create_block_mask(cfg["mask"], B, Hq, S, S, 128)
-    mask_host_ms = (time.perf_counter() - t0) * 1e3
-    bmask = pf.create_block_mask(cfg["mask"], B, Hq, S, S, 128, device=dev)
-    builds = []
-    for _ in range(5):
-        t0 = time.perf_counter()
-        pf.create_block_mask(cfg["mask"], B, Hq, S, S, 128, device=dev)
-        builds.append((time.perf_counter() - t0) * 1e3)
-    mask_ms = sorted(builds)[2]
-    if not all(np.array_equal(getattr(bmask, f), getattr(host_bmask, f))
-               for f in ("num_blocks_in_row", "col_indices", "kv_num_blocks", "kv_indices", "full_kv_num_blocks",
-                         "full_kv_indices", "q_num_blocks", "q_indices", "full_q_num_blocks", "full_q_indices")):
-        raise SystemExit("device and host block masks differ")
-    runner = Runner(tq, tk, tv, tdo, score_mod=cfg["score"], block_mask=bmask)
     pairs = count_pairs(cfg)  # per head, summed over batch rows
     flop_fwd = 4.0 * D * pairs * Hq
     flop_bwd = 10.0 * D * pairs * Hq
-    stream = torch.cuda.current_stream()
 
     if args.profile_kernel:
         runner.fwd()
@@ -259,20 +317,29 @@ def main():
         log(f"profile: {args.profile_kernel} x {args.profile_iters} on {args.config}")
         return
 
+    # block mask build: on the host and on the GPU (median of 5 device builds,
+    # each ending in the copy of the tables to the host), bit-identical
+    t0 = time.perf_counter()
+    host_bmask = pf.create_block_mask(cfg["mask"], B, Hq, S, S, 128)
+    mask_host_ms = (time.perf_counter() - t0) * 1e3
+    builds = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        pf.create_block_mask(cfg["mask"], B, Hq, S, S, 128, device=dev)
+        builds.append((time.perf_counter() - t0) * 1e3)
+    mask_ms = sorted(builds)[2]
+    if not all(np.array_equal(getattr(bmask, f), getattr(host_bmask, f))
+               for f in ("num_blocks_in_row", "col_indices", "kv_num_blocks", "kv_indices", "full_kv_num_blocks",
+                         "full_kv_indices", "q_num_blocks", "q_indices", "full_q_num_blocks", "full_q_indices")):
+        raise SystemExit("device and host block masks differ")
+
     if args.warmup is None:
-        # the clock ramps up over the first tens of milliseconds of load
-        args.warmup, t_start = 0, time.perf_counter()
-        while args.warmup < 3 or time.perf_counter() - t_start < 0.5:
-            runner.step()
-            args.warmup += 1
-            if args.warmup % 8 == 0:
-                torch.cuda.synchronize()
+        args.warmup = warm(runner.step)
     else:
         for _ in range(args.warmup):
             runner.step()
     torch.cuda.synchronize()
     log(f"warmup done ({args.warmup} steps)")
-    torch.cuda.synchronize()
     ms_step = time_region(runner.step, args.steps, stream)
     torch.cuda.synchronize()
     log(f"timed {args.steps} steps: {ms_step:.3f} ms/step")
@@ -286,20 +353,26 @@ def main():
     algo = {"fwd": flop_fwd, "bwd_dkdv": 8.0 * D * pairs * Hq, "bwd_dq": 6.0 * D * pairs * Hq}
     dom = max(("fwd", "bwd_dkdv", "bwd_dq"), key=lambda n: kernels[n])
     achieved = algo[dom] / (kernels[dom] * 1e-3) / 1e12
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", "traffic.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get(f"{args.config}/{dom}")
     fwdbwd_tflops = (flop_fwd + flop_bwd) / (ms_step * 1e-3) / 1e12
     fwd_tflops = flop_fwd / (ms_fwd * 1e-3) / 1e12
+
+    # the public API on the same inputs: flex_attention forward + autograd
+    # backward (plans, tables and device arrays cached after the first call)
+    qq, kk, vv = (t.detach().requires_grad_() for t in (tq, tk, tv))
+
+    def api_step():
+        o = pf.flex_attention(qq, kk, vv, score_mod=cfg["score"], block_mask=bmask, enable_gqa=Hq != Hkv)
+        torch.autograd.grad(o, (qq, kk, vv), tdo)
+
+    warm(api_step, min_s=0.1)
+    api_ms = time_region(api_step, args.steps, stream)
+    log(f"flex_attention fwd+bwd: {api_ms:.3f} ms/step (Runner {ms_step:.3f})")
+    del qq, kk, vv
 
     sparsity = None
     if args.dense_ref:
         dense = Runner(tq, tk, tv, tdo, score_mod=cfg["score"])
-        for _ in range(args.warmup):
-            dense.step()
-        torch.cuda.synchronize()
+        warm(dense.step, min_s=0.1)
         dense_ms = time_region(dense.step, args.steps, stream)
         del dense
         live = 1.0 - bmask.sparsity
@@ -312,6 +385,26 @@ def main():
         log("cpu baseline ...")
         cpu = cpu_baseline(cfg, arrays, pairs, args.cpu_seconds)
         log("cpu baseline done")
+    del arrays, runner, tq, tk, tv, tdo
+
+    others = {}
+    for name in [n for n in args.others.split(",") if n and n != args.config]:
+        ocfg, _, _, obm, orun = setup(name, dev, numpy_inputs=False)
+        warm(orun.step, min_s=0.1)
+        oms = time_region(orun.step, args.steps, stream)
+        orun.fwd()
+        ofwd = time_region(orun.fwd, args.steps, stream)
+        opairs = count_pairs(ocfg)
+        of, ob = 4.0 * ocfg["D"] * opairs * ocfg["Hq"], 10.0 * ocfg["D"] * opairs * ocfg["Hq"]
+        others[name] = {"workload": ocfg["workload"], "ms_per_step": round(oms, 4), "fwd_ms": round(ofwd, 4),
+                        "fwdbwd_tflops": round((of + ob) / (oms * 1e-3) / 1e12, 2),
+                        "fwdbwd_pct_peak": round(100 * (of + ob) / (oms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+                        "fwd_tflops": round(of / (ofwd * 1e-3) / 1e12, 2),
+                        "fwd_pct_peak": round(100 * of / (ofwd * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+                        "live_block_fraction": round(1.0 - obm.sparsity, 4)}
+        log(f"{name}: {others[name]['fwdbwd_tflops']} TFLOP/s fwd+bwd, {others[name]['fwd_tflops']} fwd")
+        del orun, obm
+        torch.cuda.empty_cache()
 
     out = {
         "metric": METRIC,
@@ -325,7 +418,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded numpy normals rounded to bf16)",
+        "data": "synthetic (seeded normals rounded to bf16)",
         "config": {"workload": cfg["workload"], "B": B, "Hq": Hq, "Hkv": Hkv, "S": S, "D": D,
                    "mask_block": 128, "live_tiles": bmask.live_tiles(),
                    "unmasked_pairs_per_head": pairs / B},
@@ -333,11 +426,14 @@ def main():
         "fwd_tflops": round(fwd_tflops, 2),
         "fwd_pct_peak": round(100 * fwd_tflops / PEAK_BF16_TFLOPS, 2),
         "kernel_ms": {k: round(v, 4) for k, v in kernels.items()},
+        "flex_attention_ms_per_step": round(api_ms, 4),
         "block_mask_build_ms": round(mask_ms, 3),
         "block_mask_build_host_ms": round(mask_host_ms, 2),
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic},
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": measured_traffic(args.config, dom)},
         "cpu_baseline": cpu,
+        "other_configs": others,
     }
     if sparsity is not None:
         out["sparsity_check"] = sparsity

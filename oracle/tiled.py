@@ -26,7 +26,7 @@ def _load():
         i = ctypes.c_int
         lib.ref_fwd.argtypes = [fp, fp, fp, i, i, i, i, i, i, i, i, i, ip, i, i, fp, fp, i, i, i]
         lib.ref_fwd.restype = i
-        lib.ref_bwd.argtypes = [fp, fp, fp, fp, fp, fp, i, i, i, i, i, i, i, i, i, ip, i, i, fp, fp, fp, i, i, i]
+        lib.ref_bwd.argtypes = [fp, fp, fp, fp, fp, fp, i, i, i, i, i, i, i, i, i, ip, i, i, i, fp, fp, fp, i, i, i]
         lib.ref_bwd.restype = i
         _lib = lib
     return _lib
@@ -69,8 +69,11 @@ def fwd(q, k, v, block_r=64, block_c=64, window=None, doc_ids=None, bf16=False,
 
 
 def bwd(q, k, v, o, lse, do, block_r=64, block_c=64, window=None, doc_ids=None, bf16=False,
-        stats_in_dtype=True, nthreads=0, bh_range=None):
-    """Reference three-kernel backward.  Returns (dq, dk, dv) float32."""
+        stats_in_dtype=True, nthreads=0, bh_range=None, ds_scale_after=False):
+    """Reference three-kernel backward.  Returns (dq, dk, dv) float32.
+    ``ds_scale_after`` rounds dS before the softmax scale is applied (the
+    MI355X kernels' cast point) instead of after (the reference's,
+    ``flash_attn.py:243-245,347-349``)."""
     q, k, v, o, lse, do = (_f32(a) for a in (q, k, v, o, lse, do))
     B, H, T, D = q.shape
     dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
@@ -78,7 +81,8 @@ def bwd(q, k, v, o, lse, do, block_r=64, block_c=64, window=None, doc_ids=None, 
     b0, b1 = bh_range if bh_range else (0, B * H)
     rc = _load().ref_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), _ptr(do), B, H, T, D, block_r,
                          block_c, use, left, right, None if doc is None else _ptr(doc, ctypes.c_int),
-                         int(bf16), int(stats_in_dtype), _ptr(dq), _ptr(dk), _ptr(dv), nthreads, b0, b1)
+                         int(bf16), int(stats_in_dtype), int(ds_scale_after), _ptr(dq), _ptr(dk), _ptr(dv),
+                         nthreads, b0, b1)
     if rc != 0:
         raise ValueError("ref_bwd rejected its arguments")
     return dq, dk, dv

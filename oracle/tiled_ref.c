@@ -19,6 +19,9 @@
  *   bwd dQ         :313-356 program (b*h, q-block), loop over ALL kv blocks (:355):
  *                  dQ += dS K with dS cast (:349).
  * "cast" means round-to-nearest-even to bfloat16 when bf16 != 0, identity for fp32.
+ * ds_scale_after != 0 moves the softmax scale of dS after its cast (dS rounded
+ * as P (dP - Delta), then multiplied by the scale in fp32): the cast point of
+ * the MI355X kernels, which apply the scale once to the dQ / dK accumulators.
  * Inputs are float32 arrays holding values already representable in the input
  * dtype.  Tiles that run past T are masked past the end (the reference has no
  * defined behaviour there).  Masks: window (left, right; -1 = unlimited, as
@@ -130,7 +133,8 @@ int ref_fwd(const float *q, const float *k, const float *v, int B, int H, int T,
 
 int ref_bwd(const float *q, const float *k, const float *v, const float *o, const float *lse,
             const float *dout, int B, int H, int T, int D, int block_r, int block_c, int use_mask,
-            int left, int right, const int *doc, int bf16, int stats_in_dtype, float *dq, float *dk,
+            int left, int right, const int *doc, int bf16, int stats_in_dtype, int ds_scale_after,
+            float *dq, float *dk,
             float *dv, int nthreads, int bh_begin, int bh_end) {
   if (block_r <= 0 || block_c <= 0 || D <= 0 || T <= 0) return -1;
   mask_t m = {use_mask, left, right, doc};
@@ -175,7 +179,8 @@ int ref_bwd(const float *q, const float *k, const float *v, const float *o, cons
             const float pv = expf(sv - lh[q0 + r]);
             const float dp = dotf(dor, vh + (size_t)ki * D, D);
             p[r * block_c + c] = cast_in(pv, bf16);
-            ds[r * block_c + c] = cast_in(pv * (dp - dh[q0 + r]) * scale, bf16);
+            ds[r * block_c + c] = ds_scale_after ? cast_in(pv * (dp - dh[q0 + r]), bf16) * scale
+                                                 : cast_in(pv * (dp - dh[q0 + r]) * scale, bf16);
           }
         }
         for (int c = 0; c < nc; ++c) {
@@ -216,7 +221,8 @@ int ref_bwd(const float *q, const float *k, const float *v, const float *o, cons
             if (!allowed(&m, b, T, q0 + r, ki)) sv = -INFINITY;
             const float pv = expf(sv - lh[q0 + r]);
             const float dp = dotf(dor, vh + (size_t)ki * D, D);
-            const float dsv = cast_in(pv * (dp - dh[q0 + r]) * scale, bf16);
+            const float dsv = ds_scale_after ? cast_in(pv * (dp - dh[q0 + r]), bf16) * scale
+                                             : cast_in(pv * (dp - dh[q0 + r]) * scale, bf16);
             if (dsv != 0.f) {
               const float *kr = kh + (size_t)ki * D;
               for (int d = 0; d < D; ++d) aq[d] += dsv * kr[d];

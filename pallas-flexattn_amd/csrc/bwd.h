@@ -251,7 +251,9 @@ __global__ __launch_bounds__(NW * 64) void dkdv_kernel(BwdArgs a) {
     if (tid < BQ) {
       const int qi = qbase + tid;
       const size_t ri = (size_t)(b * P.Hq + hq) * P.Sq + qi;
-      lse_st = qi < P.Sq ? a.lse[ri] * kLog2e : INFINITY;
+      // rows past Sq and rows with no live key (LSE = -inf): P = 0
+      const float l = qi < P.Sq ? a.lse[ri] : -INFINITY;
+      lse_st = l > -INFINITY ? l * kLog2e : INFINITY;
       dl_st = qi < P.Sq ? a.delta[ri] : 0.f;
     }
   };
@@ -427,7 +429,9 @@ __global__ __launch_bounds__(NW * 64) void dq_kernel(BwdArgs a) {
     df[s] = ld_frag<T>(dop + (size_t)qw * D + 16 * s + 8 * hh, qvalid);
   }
   const size_t rowi = (size_t)head * P.Sq + qw;
-  const float lse2 = qvalid ? a.lse[rowi] * kLog2e : INFINITY;
+  // a row with no live key (LSE = -inf) gets P = 0 everywhere, like rows past Sq
+  const float lse_row = qvalid ? a.lse[rowi] : -INFINITY;
+  const float lse2 = lse_row > -INFINITY ? lse_row * kLog2e : INFINITY;
   const float dl = qvalid ? a.delta[rowi] : 0.f;
   const float slope = P.alibi ? P.alibi[h] : 0.f;
   const int qdoc = (P.q_doc && qvalid) ? P.q_doc[(size_t)b * P.Sq + qw] : 0;

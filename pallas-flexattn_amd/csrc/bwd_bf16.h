@@ -142,7 +142,8 @@ __device__ __forceinline__ void zero(f32x16& x) {
 
 // ------------------------------------------------------------------- dQ ----
 template <int D, int BN, int NW, bool kMods>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void dq_bf16_kernel(BwdArgs a) {
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(occupancy_for(4 * BN * D * 2, NW, 2))))
+void dq_bf16_kernel(BwdArgs a) {
   using E = Elt<uint16_t>;
   using frag = E::frag;
   constexpr int BM = 32 * NW;
@@ -177,7 +178,9 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     }
   }
   const size_t rowi = (size_t)head * P.Sq + qw;
-  const float lse2 = qvalid ? a.lse[rowi] * kLog2e : INFINITY;
+  // a row with no live key (LSE = -inf) gets P = 0 everywhere, like rows past Sq
+  const float lse_row = qvalid ? a.lse[rowi] : -INFINITY;
+  const float lse2 = lse_row > -INFINITY ? lse_row * kLog2e : INFINITY;
   const float dl = qvalid ? a.delta[rowi] : 0.f;
   const float slope = P.alibi ? P.alibi[h] : 0.f;
   const float cap_inv = P.softcap > 0.f ? 1.0f / P.softcap : 0.f;

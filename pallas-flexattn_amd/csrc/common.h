@@ -92,6 +92,15 @@ __device__ __forceinline__ int tr_swz(int r) {
   else return 0;
 }
 
+// Waves per SIMD a kernel can reach when its workgroup of NW waves holds
+// lds_bytes of LDS (160 KiB per CU, four SIMDs), capped at `want`: the
+// occupancy target given to the register allocator.
+constexpr int occupancy_for(int lds_bytes, int nw, int want) {
+  const int wg_per_cu = (160 * 1024) / lds_bytes;
+  const int per_simd = wg_per_cu * nw / 4;
+  return per_simd < 1 ? 1 : (per_simd > want ? want : per_simd);
+}
+
 // Load through the scalar data cache (the address must be wave-uniform).
 __device__ __forceinline__ int scalar_load(const int* p, int i) {
   typedef const __attribute__((address_space(4))) int* cptr;

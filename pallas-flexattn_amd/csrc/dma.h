@@ -51,14 +51,20 @@ __device__ __forceinline__ u32x4 buf_load16(i32x4 rsrc, int byte_off) {
 // and a workgroup barrier before any wave reads the tile.  The compiler's own
 // vmcnt waits stay correct: loads counted in order only complete later when
 // unknown copies are queued behind them.
+//
+// M0 is a register the compiler reserves, so the asm saves it in a scratch
+// SGPR and puts it back after the copy (the copy takes M0 when it issues).
 __device__ __forceinline__ void dma16(i32x4 rsrc, int byte_off, char* lds_wave_base) {
   // the low 32 bits of a flat pointer into the shared aperture are the LDS
   // byte address
   const uint32_t m0v = __builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)lds_wave_base);
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
-               :
-               : "v"(byte_off), "s"(rsrc), "s"(m0v)
-               : "memory", "m0");
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(byte_off), "s"(rsrc), "s"(m0v)
+      : "memory");
 }
 
 // s_waitcnt vmcnt(0) (expcnt, lgkmcnt left at their maxima) through the

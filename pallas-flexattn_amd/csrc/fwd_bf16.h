@@ -38,7 +38,7 @@
 namespace fa {
 
 template <int D, int BN, int NW, bool kMods>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(occupancy_for(4 * BN * D * 2, NW, 2))))
 void fwd_bf16_kernel(FwdArgs a) {
   using E = Elt<uint16_t>;
   using frag = E::frag;

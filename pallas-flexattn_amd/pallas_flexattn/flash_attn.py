@@ -78,11 +78,13 @@ def _check_inputs(q, k, v):
 
 class _Plan:
     """Everything the C ABI needs besides the tensors: an fa_params struct
-    plus the device arrays its pointers refer to (kept alive here)."""
+    plus the device arrays its pointers refer to (kept alive here).  Plans
+    are cached (:func:`_get_plan`): a call with the same shapes, mask, score
+    mod, scale, block mask and tiles reuses the struct and the device arrays,
+    so repeated calls make no host-to-device copies."""
 
     def __init__(self, q, k, mask: Optional[MaskSpec], score: Optional[ScoreSpec], scale: Optional[float],
                  block_mask: Optional[BlockMask], tiles: Tuple[int, int]):
-        torch = _torch()
         B, Hq, Sq, D = q.shape
         Hkv, Skv = k.shape[1], k.shape[2]
         code, dname = _dtype_code(q)
@@ -98,28 +100,16 @@ class _Plan:
         if mask is not None:
             p.window_left, p.window_right = mask.left, mask.right
             if mask.doc_ids is not None:
-                docs = mask.doc_ids
-                if docs.shape[1] < max(Sq, Skv):
-                    raise ValueError("document ids are shorter than the sequence")
-                if docs.shape[0] not in (1, B):
-                    raise ValueError("document ids must have 1 or B rows")
-                dq_ = np.array(np.broadcast_to(docs[:, :Sq], (B, Sq)), dtype=np.int32)
-                dk_ = np.array(np.broadcast_to(docs[:, :Skv], (B, Skv)), dtype=np.int32)
-                tq = torch.from_numpy(dq_).to(dev)
-                tk = torch.from_numpy(dk_).to(dev)
-                self.keep += [tq, tk]
-                p.q_doc_ids, p.kv_doc_ids = tq.data_ptr(), tk.data_ptr()
-                bounds = mask.doc_bounds()
-                if bounds is not None and Sq == Skv and docs.shape[1] == Sq:
-                    ts, te = (torch.from_numpy(np.array(np.broadcast_to(x, (B, Sq)), dtype=np.int32)).to(dev)
-                              for x in bounds)
-                    self.keep += [ts, te]
-                    p.doc_start, p.doc_end = ts.data_ptr(), te.data_ptr()
+                arrs = mask.device_doc_arrays(dev, B, Sq, Skv)
+                self.keep.append(arrs)
+                p.q_doc_ids, p.kv_doc_ids = arrs["q"].data_ptr(), arrs["kv"].data_ptr()
+                if "start" in arrs:
+                    p.doc_start, p.doc_end = arrs["start"].data_ptr(), arrs["end"].data_ptr()
         if score is not None:
             if score.alibi is not None:
                 if score.alibi.shape[0] != Hq:
                     raise ValueError(f"ALiBi needs one slope per q head ({Hq}), got {score.alibi.shape[0]}")
-                ts = torch.from_numpy(score.alibi).to(dev)
+                ts = score.device_slopes(dev)
                 self.keep.append(ts)
                 p.alibi_slopes = ts.data_ptr()
             p.softcap = score.softcap
@@ -134,6 +124,7 @@ class _Plan:
             if tb not in (1, B) or th not in (1, Hq):
                 raise ValueError("block mask tables do not broadcast over (B, H)")
             t = block_mask.device_tables(dev)
+            self.keep.append(t)
             p.mask_block_q = p.mask_block_kv = bs
             p.table_b, p.table_h = tb, th
             p.kv_width = t["kv_indices"].shape[-1]
@@ -142,10 +133,32 @@ class _Plan:
                 setattr(p, name, t[name].data_ptr())
         self.params = p
         self.dname = dname
+        import ctypes
+        self._ref = ctypes.byref(self.params)
 
     def ptr(self):
-        import ctypes
-        return ctypes.byref(self.params)
+        return self._ref
+
+
+_PLAN_CACHE = {}
+_PLAN_CACHE_MAX = 128
+
+
+def _get_plan(q, k, mask, score, scale, block_mask, tiles) -> _Plan:
+    """Cached :class:`_Plan` for this call.  Keyed on everything the struct
+    depends on; a block mask is keyed by identity and the cache entry holds a
+    reference to it, so the key stays unique while the entry lives."""
+    key = (tuple(q.shape), tuple(k.shape), q.dtype, str(q.device),
+           None if mask is None else mask.key(), None if score is None else score.key(),
+           scale, None if block_mask is None else id(block_mask), tuple(tiles))
+    hit = _PLAN_CACHE.get(key)
+    if hit is not None and hit[1] is block_mask:
+        return hit[0]
+    plan = _Plan(q, k, mask, score, scale, block_mask, tiles)
+    if len(_PLAN_CACHE) >= _PLAN_CACHE_MAX:
+        _PLAN_CACHE.pop(next(iter(_PLAN_CACHE)))
+    _PLAN_CACHE[key] = (plan, block_mask)
+    return plan
 
 
 _MASK_CACHE = {}
@@ -199,32 +212,37 @@ def _dense16(t):
 
 
 def _fwd_core(q, k, v, mask, score, scale, block_mask, tiles):
+    """Forward through fa_fwd -> (o, lse fp32, plan)."""
     torch = _torch()
     _check_inputs(q, k, v)
     q, k, v = _dense16(q), _dense16(k), _dense16(v)
     if block_mask is None and mask is not None and not mask.is_trivial:
         block_mask = _internal_block_mask(mask, q.shape[0], q.shape[2], k.shape[2], q.device)
-    plan = _Plan(q, k, mask, score, scale, block_mask, tiles)
+    plan = _get_plan(q, k, mask, score, scale, block_mask, tiles)
     o = torch.empty_like(q)
     lse = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
     lib = _lib.load()
     _lib.check(lib.fa_fwd(plan.ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
                           _stream()))
-    return o, lse
+    return o, lse, plan
 
 
-def _bwd_core(q, k, v, o, lse, do, mask, score, scale, block_mask, tiles):
+def _bwd_core(q, k, v, o, lse, do, mask, score, scale, block_mask, tiles, plan=None):
+    """Backward through fa_bwd -> (dq, dk, dv).  ``plan`` is the forward's
+    plan when the caller has it (same problem), else one is looked up."""
     torch = _torch()
     _check_inputs(q, k, v)
     if do.dtype != q.dtype:
         do = do.to(q.dtype)
     q, k, v, o, do = (_dense16(t) for t in (q, k, v, o, do))
-    lse = lse.to(torch.float32).contiguous()
+    if lse.dtype != torch.float32 or not lse.is_contiguous():
+        lse = lse.to(torch.float32).contiguous()
     if o.shape != q.shape or do.shape != q.shape or lse.shape != q.shape[:3]:
         raise ValueError("o / do / lse shapes do not match q")
-    if block_mask is None and mask is not None and not mask.is_trivial:
-        block_mask = _internal_block_mask(mask, q.shape[0], q.shape[2], k.shape[2], q.device)
-    plan = _Plan(q, k, mask, score, scale, block_mask, tiles)
+    if plan is None:
+        if block_mask is None and mask is not None and not mask.is_trivial:
+            block_mask = _internal_block_mask(mask, q.shape[0], q.shape[2], k.shape[2], q.device)
+        plan = _get_plan(q, k, mask, score, scale, block_mask, tiles)
     lib = _lib.load()
     ws_bytes = lib.fa_bwd_workspace_bytes(plan.ptr())
     ws = torch.empty(max(ws_bytes, 256), device=q.device, dtype=torch.uint8)
@@ -237,9 +255,15 @@ def _bwd_core(q, k, v, o, lse, do, mask, score, scale, block_mask, tiles):
     return dq, dk, dv
 
 
-def _ref_tiles(q, block_r, block_c):
+def _sparse(mask) -> bool:
+    return mask is not None and not mask.is_trivial
+
+
+def _ref_tiles(q, block_r, block_c, sparse=False):
+    """Kernel tile of a reference-signature call: block_r / block_c are
+    Triton hints; the tuned tile for the shape class (or the default) runs."""
     _, dname = _dtype_code(q)
-    return kernel_tiles(block_r, block_c, dname)
+    return kernel_tiles(block_r, block_c, dname, q.shape[2], q.shape[3], sparse)
 
 
 def _as4d(t):
@@ -252,7 +276,7 @@ def _stage_plan(q4, k4, mask_mod, block_r, block_c, scale=None):
     bm = None
     if mask is not None and not mask.is_trivial:
         bm = _internal_block_mask(mask, q4.shape[0], q4.shape[2], k4.shape[2], q4.device)
-    return _Plan(q4, k4, mask, None, scale, bm, _ref_tiles(q4, block_r, block_c))
+    return _get_plan(q4, k4, mask, None, scale, bm, _ref_tiles(q4, block_r, block_c, bm is not None))
 
 
 def flash_attention_bwd_preprocess(o_flat, do_flat, block_r: int = DEFAULT_BLOCK_R,
@@ -390,7 +414,8 @@ def flash_attention_fwd(q, k, v, mask_mod: Optional[MaskMod] = None, block_r: in
                         num_stages: int = DEFAULT_NUM_STAGES, interpret: bool = False):
     """Forward pass -> (o, logsumexp) with logsumexp in q's dtype (``flash_attn.py:111-165``)."""
     _check_interpret(interpret)
-    o, lse = _fwd_core(q, k, v, _as_mask_spec(mask_mod), None, None, None, _ref_tiles(q, block_r, block_c))
+    mask = _as_mask_spec(mask_mod)
+    o, lse, _ = _fwd_core(q, k, v, mask, None, None, None, _ref_tiles(q, block_r, block_c, _sparse(mask)))
     return o, lse.to(q.dtype)
 
 
@@ -401,8 +426,9 @@ def flash_attention_bwd(q, k, v, o, logsumexp, do, mask_mod: Optional[MaskMod] =
     """Backward pass -> (dq, dk, dv) (``flash_attn.py:410-461``).  ``logsumexp``
     may be in q's dtype (as returned by :func:`flash_attention_fwd`) or fp32."""
     _check_interpret(interpret)
-    return _bwd_core(q, k, v, o, logsumexp, do, _as_mask_spec(mask_mod), None, None, None,
-                     _ref_tiles(q, block_r, block_c))
+    mask = _as_mask_spec(mask_mod)
+    return _bwd_core(q, k, v, o, logsumexp, do, mask, None, None, None,
+                     _ref_tiles(q, block_r, block_c, _sparse(mask)))
 
 
 class _FlexFn:
@@ -418,16 +444,17 @@ class _FlexFn:
             class FlexAttnFunction(torch.autograd.Function):
                 @staticmethod
                 def forward(ctx, q, k, v, cfg):
-                    o, lse = _fwd_core(q, k, v, *cfg)
+                    o, lse, plan = _fwd_core(q, k, v, *cfg)
                     ctx.save_for_backward(q, k, v, o, lse)
                     ctx.cfg = cfg
+                    ctx.plan = plan
                     ctx.mark_non_differentiable(lse)
                     return o, lse
 
                 @staticmethod
                 def backward(ctx, do, dlse):
                     q, k, v, o, lse = ctx.saved_tensors
-                    dq, dk, dv = _bwd_core(q, k, v, o, lse, do, *ctx.cfg)
+                    dq, dk, dv = _bwd_core(q, k, v, o, lse, do, *ctx.cfg, plan=ctx.plan)
                     return dq, dk, dv, None
 
             cls.fn = FlexAttnFunction
@@ -439,7 +466,8 @@ def flash_attention(q, k, v, mask_mod: Optional[MaskMod] = None, block_r: int = 
                     num_stages: int = DEFAULT_NUM_STAGES, interpret: bool = False):
     """Flash attention with a custom backward (``flash_attn.py:464-504``)."""
     _check_interpret(interpret)
-    cfg = (_as_mask_spec(mask_mod), None, None, None, _ref_tiles(q, block_r, block_c))
+    mask = _as_mask_spec(mask_mod)
+    cfg = (mask, None, None, None, _ref_tiles(q, block_r, block_c, _sparse(mask)))
     o, _ = _FlexFn.get().apply(q, k, v, cfg)
     return o
 
@@ -464,7 +492,7 @@ def flex_decode(query, key, value, score_mod: Optional[ScoreSpec] = None, block_
     q, k, v = _dense16(query), _dense16(key), _dense16(value)
     _check_inputs(q, k, v)
     _, dname = _dtype_code(q)
-    plan = _Plan(q, k, mask, _as_score_spec(score_mod), scale, block_mask, (128, 64 if dname == "bf16" else 32))
+    plan = _get_plan(q, k, mask, _as_score_spec(score_mod), scale, block_mask, (128, 64 if dname == "bf16" else 32))
     o = torch.empty_like(q)
     lse = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
     lib = _lib.load()

@@ -3,14 +3,11 @@
 ``get_optimal_params`` / ``get_kernel_config`` / ``print_kernel_config`` keep
 the reference's static table and signatures (``kernel_tuner.py:11-148``).
 Their four numbers are the reference's Triton knobs; :func:`kernel_tiles`
-maps them onto the MI355X kernels' tile choices:
-
-* ``block_r``  -> query tile BLOCK_M of the forward / dQ kernels (64 or 128;
-  each wave owns 32 query rows, so BLOCK_M / 32 waves per workgroup),
-* ``block_c``  -> key tile BLOCK_N (bf16: 64, fp32: 32 — the tiles the LDS
-  layout is built for),
-* ``num_warps``/``num_stages`` are accepted and recorded; wave count follows
-  BLOCK_M and the kernels double-buffer through registers.
+takes them as hints only: the gfx950 tile of a call (BLOCK_M query rows,
+32 per wave, BLOCK_N keys per LDS tile) is the one :func:`tune` measured
+fastest for the shape class, else the default 128 x 64 (bf16) / 128 x 32
+(fp32).  ``num_warps`` / ``num_stages`` are accepted for signature
+compatibility; the wave count follows BLOCK_M.
 
 :func:`tune` measures the available instantiations on the current GPU and
 stores the winners in a JSON table that ``flex_attention`` consults.
@@ -124,33 +121,56 @@ def print_kernel_config(
 # -- MI355X tile selection ----------------------------------------------------
 SUPPORTED_BLOCK_M = (64, 128)
 SUPPORTED_BLOCK_N = {"bf16": (64,), "fp32": (32,)}
+DEFAULT_TILES = {"bf16": (128, 64), "fp32": (128, 32)}
 
 
-def kernel_tiles(block_r: int, block_c: int, dtype: str) -> Tuple[int, int]:
-    """Map the reference's (block_r, block_c) onto an instantiated
-    (BLOCK_M, BLOCK_N): the largest supported BLOCK_M not above
-    max(block_r, 64), and the dtype's key tile."""
-    bm = 128 if block_r >= 128 else 64
-    bn = SUPPORTED_BLOCK_N[dtype][0]
-    return bm, bn
+def kernel_tiles(block_r: int, block_c: int, dtype: str, seq_len: Optional[int] = None,
+                 head_dim: Optional[int] = None, sparse: bool = False) -> Tuple[int, int]:
+    """(BLOCK_M, BLOCK_N) for a call that came with the reference's Triton
+    tile hints ``block_r`` / ``block_c``.  The hints describe a Triton
+    schedule on another GPU, so they do not pick the gfx950 tile: the tile
+    recorded by :func:`tune` for this shape class is used when there is one,
+    else the default (128 queries x 64 keys for bf16, 128 x 32 for fp32),
+    which measured fastest on every shape tuned so far."""
+    if seq_len is not None and head_dim is not None:
+        t = tuned_tiles(seq_len, head_dim, dtype, sparse)
+        if t is not None:
+            return t
+    return DEFAULT_TILES[dtype]
 
 
 TUNE_TABLE = os.environ.get(
     "FLEXATTN_TUNE_TABLE", os.path.join(os.path.dirname(os.path.abspath(__file__)), "tune_table.json"))
 
+_TABLE_CACHE: Dict[str, Tuple[float, Dict]] = {}
+
 
 def load_tune_table(path: str = TUNE_TABLE) -> Dict[str, Dict[str, int]]:
-    if not os.path.exists(path):
+    """The tuner's JSON table (empty if absent), parsed once per file
+    modification time."""
+    try:
+        mtime = os.path.getmtime(path)
+    except OSError:
         return {}
+    hit = _TABLE_CACHE.get(path)
+    if hit is not None and hit[0] == mtime:
+        return hit[1]
     with open(path) as f:
-        return json.load(f)
+        table = json.load(f)
+    _TABLE_CACHE[path] = (mtime, table)
+    return table
+
+
+def table_key(seq_len: int, head_dim: int, dtype: str, sparse: bool) -> str:
+    """Key of a shape class.  "sparse" entries were measured with a causal
+    block mask and serve every call that has a block mask (window, document
+    and causal masks alike); "dense" ones serve calls without a mask."""
+    return f"{dtype}/D{head_dim}/S{seq_len}/{'sparse' if sparse else 'dense'}"
 
 
 def tuned_tiles(seq_len: int, head_dim: int, dtype: str, sparse: bool) -> Optional[Tuple[int, int]]:
     """Tiles recorded by :func:`tune` for this shape class, if any."""
-    table = load_tune_table()
-    key = f"{dtype}/D{head_dim}/S{seq_len}/{'sparse' if sparse else 'dense'}"
-    e = table.get(key)
+    e = load_tune_table().get(table_key(seq_len, head_dim, dtype, sparse))
     return (e["block_m"], e["block_n"]) if e else None
 
 
@@ -211,10 +231,19 @@ def tune(batch: int = 4, heads: int = 32, seq_len: int = 4096, head_dim: int = 1
         torch.cuda.synchronize()
         return s.elapsed_time(e) / iters
 
-    results = {}
+    # every candidate's output is checked against the default tile's before it
+    # can be recorded: a tile whose kernel disagrees is skipped, not chosen
+    base_opts = {"BLOCK_M": DEFAULT_TILES[dtype][0], "BLOCK_N": DEFAULT_TILES[dtype][1]}
+    ref = _candidate_outputs(q, k, v, do, bm_mask, base_opts)
+    tol = 2e-2 if dtype == "bf16" else 1e-5
+    results, rejected = {}, {}
     for bm in SUPPORTED_BLOCK_M:
         for bn in SUPPORTED_BLOCK_N[dtype]:
             opts = {"BLOCK_M": bm, "BLOCK_N": bn}
+            bad = _mismatch(ref, _candidate_outputs(q, k, v, do, bm_mask, opts), tol)
+            if bad:
+                rejected[f"{bm}x{bn}"] = bad
+                continue
             qq, kk, vv = (t.detach().requires_grad_() for t in (q, k, v))
 
             def fwd_only():
@@ -231,15 +260,35 @@ def tune(batch: int = 4, heads: int = 32, seq_len: int = 4096, head_dim: int = 1
                                  "tflops_fwd": round(flops_fwd / t_f / 1e9, 1),
                                  "tflops_fwd_bwd": round(3.5 * flops_fwd / t_fb / 1e9, 1),
                                  "pct_peak_fwd_bwd": round(100 * 3.5 * flops_fwd / t_fb / 1e9 / peak, 2)}
+    if not results:
+        raise RuntimeError(f"tune: every candidate disagreed with the default tile: {rejected}")
     (bm, bn), best = min(results.items(), key=lambda kv: kv[1]["ms_fwd_bwd"])
     table = load_tune_table(path)
-    key = f"{dtype}/D{head_dim}/S{seq_len}/{'sparse' if causal else 'dense'}"
+    key = table_key(seq_len, head_dim, dtype, causal)
     table[key] = {"block_m": bm, "block_n": bn, "ms_fwd_bwd": best["ms_fwd_bwd"],
                   "shape": f"B{batch} H{heads} S{seq_len} D{head_dim} {'causal' if causal else 'dense'}",
                   "candidates": {f"{a}x{b}": r for (a, b), r in results.items()}}
+    if rejected:
+        table[key]["rejected"] = rejected
     with open(path, "w") as f:
         json.dump(table, f, indent=1, sort_keys=True)
     return table[key]
+
+
+def _candidate_outputs(q, k, v, do, bm_mask, opts):
+    """O, LSE, dQ, dK, dV of one candidate on the first (batch, head) slice
+    of the tuning inputs (float32 copies)."""
+    from .flash_attn import flex_attention
+    sl = [t[:1, :1].detach().clone().requires_grad_() for t in (q, k, v)]
+    o, lse = flex_attention(*sl, block_mask=bm_mask, kernel_options=opts, return_lse=True)
+    o.backward(do[:1, :1])
+    return [t.detach().float() for t in (o, lse, sl[0].grad, sl[1].grad, sl[2].grad)]
+
+
+def _mismatch(ref, got, tol):
+    """Names of the outputs outside atol = rtol = tol of the reference ones."""
+    names = ("O", "LSE", "dQ", "dK", "dV")
+    return [n for n, a, b in zip(names, ref, got) if not bool(((a - b).abs() <= tol + tol * a.abs()).all())]
 
 
 if __name__ == "__main__":

@@ -46,6 +46,7 @@ class MaskSpec:
         self.doc_ids = doc_ids
         self.name = name or self._default_name()
         self._torch_docs = {}
+        self._device_docs = {}
 
     def _default_name(self):
         parts = []
@@ -93,9 +94,37 @@ class MaskSpec:
         return self._bounds
 
     def key(self):
-        """Hashable identity (used for caching block masks)."""
-        docs = None if self.doc_ids is None else (self.doc_ids.shape, hash(self.doc_ids.tobytes()))
-        return ("MaskSpec", self.left, self.right, docs)
+        """Hashable identity (used for caching block masks and kernel plans);
+        computed once, the descriptor is immutable."""
+        k = self.__dict__.get("_key")
+        if k is None:
+            docs = None if self.doc_ids is None else (self.doc_ids.shape, hash(self.doc_ids.tobytes()))
+            k = self._key = ("MaskSpec", self.left, self.right, docs)
+        return k
+
+    def device_doc_arrays(self, device, B: int, Sq: int, Skv: int):
+        """int32 device arrays the kernels read for a document mask, cached per
+        (device, B, Sq, Skv): "q" (B, Sq) and "kv" (B, Skv) ids, plus "start" /
+        "end" (B, Sq) run bounds when documents are contiguous runs of one
+        self-attention sequence (masks are then intervals for the kernels)."""
+        ck = (str(device), B, Sq, Skv)
+        arrs = self._device_docs.get(ck)
+        if arrs is not None:
+            return arrs
+        import torch
+        docs = self.doc_ids
+        if docs.shape[1] < max(Sq, Skv):
+            raise ValueError("document ids are shorter than the sequence")
+        if docs.shape[0] not in (1, B):
+            raise ValueError("document ids must have 1 or B rows")
+        arrs = {"q": torch.from_numpy(np.array(np.broadcast_to(docs[:, :Sq], (B, Sq)), dtype=np.int32)).to(device),
+                "kv": torch.from_numpy(np.array(np.broadcast_to(docs[:, :Skv], (B, Skv)), dtype=np.int32)).to(device)}
+        bounds = self.doc_bounds()
+        if bounds is not None and Sq == Skv and docs.shape[1] == Sq:
+            arrs["start"], arrs["end"] = (
+                torch.from_numpy(np.array(np.broadcast_to(x, (B, Sq)), dtype=np.int32)).to(device) for x in bounds)
+        self._device_docs[ck] = arrs
+        return arrs
 
     def __eq__(self, other):
         return isinstance(other, MaskSpec) and self.key() == other.key()

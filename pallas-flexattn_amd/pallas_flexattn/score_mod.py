@@ -40,6 +40,14 @@ class ScoreSpec:
     def key(self):
         return ("ScoreSpec", None if self.alibi is None else self.alibi.tobytes(), self.softcap)
 
+    def device_slopes(self, device):
+        """The ALiBi slopes as a float32 tensor on ``device`` (cached)."""
+        import torch
+        dev = torch.device(device)
+        if dev not in self._torch_slopes:
+            self._torch_slopes[dev] = torch.as_tensor(self.alibi, device=dev)
+        return self._torch_slopes[dev]
+
     def __eq__(self, other):
         return isinstance(other, ScoreSpec) and self.key() == other.key()
 

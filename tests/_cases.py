@@ -67,3 +67,17 @@ def oracle_fwd_bwd(q, k, v, do, mask, scale=None, alibi=None, softcap=None, bwd=
     if not bwd:
         return o, lse, None
     return o, lse, attention.backward(q, k, v, do, mask=mask, scale=scale, alibi_slopes=alibi, softcap=softcap)
+
+
+def assert_as_accurate(name, got, alg, exact, max_ratio=1.5, rms_ratio=1.25):
+    """`got` is no further from `exact` than `alg` (the reference's algorithm
+    restated with its bf16 cast points) is: max and RMS errors against the
+    float64 result within the given ratios of the algorithm's own.  For inputs
+    where the algorithm's bf16 roundings, not the implementation, set the
+    error (large logits: dS values that cancel in the dQ / dK sums)."""
+    got, alg, exact = (np.asarray(x, dtype=np.float64) for x in (got, alg, exact))
+    eg, ea = np.abs(got - exact), np.abs(alg - exact)
+    rg, ra = np.sqrt((eg ** 2).mean()), np.sqrt((ea ** 2).mean())
+    if not (eg.max() <= max_ratio * ea.max() and rg <= rms_ratio * ra):
+        raise AssertionError(f"{name}: error against float64 max {eg.max():.3g} / rms {rg:.3g}, the reference "
+                             f"algorithm's max {ea.max():.3g} / rms {ra:.3g} (allowed x{max_ratio} / x{rms_ratio})")

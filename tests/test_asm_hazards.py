@@ -12,8 +12,9 @@ instruction touching the destination of an inline-asm MFMA comes at least 20 wai
 it (`s_nop N` counts N + 1, any other instruction 1), scanning each kernel in fall-through
 order.  In the other direction, an inline-asm MFMA must not read an A or B operand that a
 compiler-emitted VALU instruction wrote fewer than 2 wait states before (the schedules that drop
-`mfma_acc`'s leading `s_nop 1` rely on this).  The same assembly must name M0 only inside inline
-asm: the LDS-DMA asm sets M0 without restoring it.  Each scan is checked on a planted case."""
+`mfma_acc`'s leading `s_nop 1` rely on this).  M0 is a register the compiler reserves: an inline
+asm block that writes M0 (the LDS-DMA copy) must save it first and put the saved value back as its
+last M0 write.  Each scan is checked on a planted case."""
 import os
 import re
 import shutil
@@ -153,28 +154,44 @@ def test_no_early_reads_of_asm_mfma_results(tmp_path):
     assert ";;#ASMSTART" in text and "v_mfma" in text
     found = early_touches(text)
     assert not found, "\n".join(f"{k} line {ln}: {ws} wait states: {ins}" for k, ln, ws, ins in found[:20])
-    # The LDS-DMA asm (csrc/dma.h) sets M0 without restoring it, which is only sound while the
-    # compiler itself keeps nothing in M0.
-    m0 = m0_uses(text)
-    assert not m0, "compiler-emitted M0 uses: " + "; ".join(m0[:10])
+    # every inline-asm block that writes M0 hands the compiler's value back
+    m0 = m0_unrestored(text)
+    assert not m0, "inline asm leaves M0 changed: " + "; ".join(m0[:10])
     late = late_operands(text)
     assert not late, "\n".join(f"{k} line {ln}: {ws} wait states: {ins}" for k, ln, ws, ins in late[:20])
 
 
-def m0_uses(asm_text):
-    """Compiler-emitted (outside inline asm) instructions that name M0."""
-    out, inasm = [], False
+def m0_unrestored(asm_text):
+    """Inline-asm blocks (their first line) that write M0 without first copying it to an SGPR
+    and ending with that SGPR copied back."""
+    out, block = [], None
     for line in asm_text.split("\n"):
-        t = line.strip()
+        t = line.strip().split(";;")[0].strip() if not line.strip().startswith(";;") else line.strip()
         if t.startswith(";;#ASMSTART"):
-            inasm = True
+            block = []
         elif t.startswith(";;#ASMEND"):
-            inasm = False
-        elif not inasm and t and not t.startswith((";", ".")) and re.search(r"\bm0\b", t.split(";")[0]):
-            out.append(t)
+            saved, last_write, ok = None, None, True
+            for ins in block:
+                m = re.match(r"s_mov_b32\s+(s\d+),\s*m0$", ins)
+                if m and saved is None and last_write is None:
+                    saved = m.group(1)
+                    continue
+                m = re.match(r"s_mov_b32\s+m0,\s*(\S+)$", ins)
+                if m:
+                    last_write = m.group(1)
+                elif re.search(r"^\S+\s+m0\b", ins):  # any other instruction writing M0
+                    last_write = "?"
+            if last_write is not None and (saved is None or last_write != saved):
+                out.append(block[0] if block else "")
+            block = None
+        elif block is not None and t:
+            block.append(t)
     return out
 
 
-def test_m0_scan_finds_planted_use():
-    asm = "\t;;#ASMSTART\n\ts_mov_b32 m0, s4\n\t;;#ASMEND\n\ts_mov_b32 m0, -1\n\tds_write_b32 v1, v2\n"
-    assert m0_uses(asm) == ["s_mov_b32 m0, -1"]
+def test_m0_scan_finds_planted_case():
+    good = "\t;;#ASMSTART\n\ts_mov_b32 s9, m0\n\ts_mov_b32 m0, s4\n\tbuffer_load_dwordx4 v1, s[0:3], 0 offen lds\n" \
+           "\ts_mov_b32 m0, s9\n\t;;#ASMEND\n"
+    bad = "\t;;#ASMSTART\n\ts_mov_b32 m0, s4\n\tbuffer_load_dwordx4 v1, s[0:3], 0 offen lds\n\t;;#ASMEND\n"
+    assert m0_unrestored(good) == []
+    assert m0_unrestored(bad) == ["s_mov_b32 m0, s4"]

@@ -1,4 +1,4 @@
-"""GPU checks at the benchmark workloads' full sizes (C3 sliding window S=8192,
+"""GPU checks at the benchmark workloads' full sizes (C2 causal S=2048, C3 sliding window S=8192,
 C4 GQA + ALiBi + soft-cap S=4096, C5 packed documents S=16384, causal S=8192).
 
 The kernels run over every (batch, head); two (batch, kv-head) groups are then
@@ -92,7 +92,7 @@ def _close(name, got, want):
                                  f"max err {float(err.max()):.3g}")
 
 
-@pytest.mark.parametrize("name", ["c3", "c4", "c5", "ns"])
+@pytest.mark.parametrize("name", ["c2", "c3", "c4", "c5", "ns"])
 def test_fullsize_workload(name):
     import torch
     import bench

@@ -48,12 +48,28 @@ def test_threshold_table(seq, d, sparse, want):
 
 
 def test_kernel_tile_mapping():
-    assert kernel_tiles(128, 64, "bf16") == (128, 64)
-    assert kernel_tiles(64, 64, "bf16") == (64, 64)
-    assert kernel_tiles(32, 32, "bf16") == (64, 64)
-    assert kernel_tiles(128, 128, "fp32") == (128, 32)
-    for br in (32, 64, 128, 256):
-        assert kernel_tiles(br, 64, "bf16")[0] in SUPPORTED_BLOCK_M
+    """The reference's block_r / block_c are Triton hints: without a tuned entry
+    every hint maps to the default gfx950 tile; with one, the tuned tile."""
+    import json
+    import pallas_flexattn.kernel_tuner as kt
+    for br, bc in ((128, 64), (64, 64), (32, 32), (256, 128)):
+        assert kernel_tiles(br, bc, "bf16") == (128, 64)
+        assert kernel_tiles(br, bc, "fp32") == (128, 32)
+    assert kernel_tiles(64, 64, "bf16", 12345, 128, True) == (128, 64)  # no entry for this shape
+
+
+def test_kernel_tiles_follow_the_tune_table(tmp_path, monkeypatch):
+    import json
+    import pallas_flexattn.kernel_tuner as kt
+    path = tmp_path / "table.json"
+    path.write_text(json.dumps({kt.table_key(1024, 64, "bf16", True): {"block_m": 64, "block_n": 64}}))
+    monkeypatch.setattr(kt, "TUNE_TABLE", str(path))
+    monkeypatch.setattr(kt.load_tune_table, "__defaults__", (str(path),))
+    assert kt.kernel_tiles(128, 128, "bf16", 1024, 64, True) == (64, 64)
+    assert kt.kernel_tiles(128, 128, "bf16", 1024, 64, False) == (128, 64)
+    assert kt.tuned_tiles(1024, 64, "bf16", True) == (64, 64)
+    # parsed once per modification time
+    assert kt.load_tune_table(str(path)) is kt.load_tune_table(str(path))
 
 
 def test_committed_tune_table_is_consistent():

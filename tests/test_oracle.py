@@ -163,6 +163,30 @@ def test_tiled_restatement_bf16_cast_points_within_bf16_tolerance():
         np.testing.assert_allclose(g, w, atol=5e-2, rtol=5e-2)
 
 
+def test_tiled_ds_scale_after_cast_point():
+    """ds_scale_after moves only the softmax scale across the dS rounding: in
+    float32 (no rounding) the gradients are identical, in bf16 dV (which never
+    sees dS) is identical and dQ / dK stay within the bf16 tolerance of the
+    reference's cast point, and the cast itself is exercised (dQ changes; D = 128
+    makes the scale 2^-3.5, which is not exact in bf16 rounding)."""
+    B, H, T, D = 1, 2, 192, 128
+    q, k, v, do = (round_bf16(np.random.default_rng(10 + s).standard_normal((B, H, T, D)).astype(np.float32))
+                   for s in range(4))
+    for bf16 in (False, True):
+        o, lse = tiled.fwd(q, k, v, 64, 64, window=(-1, 0), bf16=bf16, stats_in_dtype=False)
+        a = tiled.bwd(q, k, v, o, lse, do, 64, 64, window=(-1, 0), bf16=bf16, stats_in_dtype=False)
+        b = tiled.bwd(q, k, v, o, lse, do, 64, 64, window=(-1, 0), bf16=bf16, stats_in_dtype=False,
+                      ds_scale_after=True)
+        if not bf16:
+            for x, y in zip(a, b):
+                np.testing.assert_allclose(x, y, rtol=1e-6, atol=1e-7)
+        else:
+            assert np.array_equal(a[2], b[2])
+            assert not np.array_equal(a[0], b[0])
+            for x, y in zip(a[:2], b[:2]):
+                np.testing.assert_allclose(x, y, atol=2e-2, rtol=2e-2)
+
+
 # --------------------------------------------------------- golden data ----
 def test_golden_fixture_reproduces():
     import os
