@@ -50,7 +50,8 @@ enum fa_status {
   FA_ERR_TABLES = -5,        /* block tables inconsistent with the sizes */
   FA_ERR_WORKSPACE = -6,     /* workspace missing or too small */
   FA_ERR_LAUNCH = -7,        /* the HIP launch failed */
-  FA_ERR_VERSION = -8        /* params.abi_version != FA_ABI_VERSION */
+  FA_ERR_VERSION = -8,       /* params.abi_version != FA_ABI_VERSION */
+  FA_ERR_TOO_LARGE = -9      /* beyond the fixed scratch of fa_bwd_noalloc */
 };
 
 /*
@@ -126,6 +127,19 @@ size_t fa_bwd_workspace_bytes(const fa_params *p);
 int fa_bwd(const fa_params *p, const void *q, const void *k, const void *v, const void *o,
            const float *lse, const void *dout, void *dq, void *dk, void *dv, void *workspace,
            size_t workspace_bytes, void *stream);
+
+/* fa_bwd without a workspace, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No reference counterpart: the reference's XLA runtime always
+ * allocated its intermediates.  Delta lives in a fixed device array of
+ * fa_bwd_noalloc_max_rows() floats (8M: 32 MiB per GPU, held from the
+ * library's first use on a GPU until the process ends); problems with
+ * B * Hq * Sq above that return FA_ERR_TOO_LARGE.  Same kernels and results
+ * as fa_bwd.  Calls on one GPU share that array: calls that overlap in time
+ * on the same GPU (different streams, or threads) race and must not be made. */
+size_t fa_bwd_noalloc_max_rows(void);
+int fa_bwd_noalloc(const fa_params *p, const void *q, const void *k, const void *v, const void *o,
+                   const float *lse, const void *dout, void *dq, void *dk, void *dv, void *stream);
 
 /* The three stages fa_bwd runs, callable one at a time (the reference exposes
  * the same split as flash_attention_bwd_preprocess / _dkv / _dq).

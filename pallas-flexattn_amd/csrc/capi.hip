@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <initializer_list>
+#include <mutex>
 
 #include "../../include/flexattn.h"
 #include "bwd.h"
@@ -256,6 +257,32 @@ size_t delta_bytes(const fa_params* p) {
   return ((size_t)p->B * p->Hq * p->Sq * sizeof(float) + 255) & ~(size_t)255;
 }
 
+// ------------------------------------------------ allocation-free bwd ----
+// fa_bwd_noalloc keeps its Delta rows (B * Hq * Sq floats) in this array
+// instead of a caller workspace: 32 MiB per GPU, held from the library's
+// first use on that GPU until the process ends.  In host code `scratch` is
+// only a handle: its device address on the current GPU comes from
+// hipGetSymbolAddress, taken once per device and kept in scratch_ptr.
+constexpr size_t kScratchFloats = size_t(8) << 20;
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+float* scratch_ptr[kMaxDevices] = {nullptr};
+
+// Device address of this device's scratch array (nullptr on failure).
+float* device_scratch() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+    scratch_ptr[dev] = static_cast<float*>(ptr);
+  }
+  return scratch_ptr[dev];
+}
+
 // ------------------------------------------------------ block masks ----
 struct MaskLayout {
   int nq, nk;
@@ -327,6 +354,7 @@ const char* fa_strerror(int status) {
     case FA_ERR_WORKSPACE: return "workspace missing or too small";
     case FA_ERR_LAUNCH: return "HIP kernel launch failed";
     case FA_ERR_VERSION: return "fa_params.abi_version does not match the library";
+    case FA_ERR_TOO_LARGE: return "B * Hq * Sq exceeds fa_bwd_noalloc_max_rows()";
     default: return "unknown status";
   }
 }
@@ -419,6 +447,31 @@ int fa_bwd(const fa_params* p, const void* q, const void* k, const void* v, cons
   a.dk = dk;
   a.dv = dv;
   a.delta = static_cast<float*>(workspace);
+  return bwd_stages(p, a, kStageDelta | kStageDkdv | kStageDq, static_cast<hipStream_t>(stream));
+}
+
+size_t fa_bwd_noalloc_max_rows(void) { return kScratchFloats; }
+
+int fa_bwd_noalloc(const fa_params* p, const void* q, const void* k, const void* v, const void* o,
+                   const float* lse, const void* dout, void* dq, void* dk, void* dv, void* stream) {
+  if (!p) return FA_ERR_NULL;
+  if (!q || !k || !v || !o || !lse || !dout || !dq || !dk || !dv) return FA_ERR_NULL;
+  if (!aligned16({q, k, v, o, dout, dq, dk, dv})) return FA_ERR_SHAPE;
+  if (p->B < 1 || p->Hq < 1 || p->Sq < 1) return FA_ERR_SHAPE;
+  if ((size_t)p->B * p->Hq * p->Sq > kScratchFloats) return FA_ERR_TOO_LARGE;
+  float* delta = device_scratch();
+  if (!delta) return FA_ERR_LAUNCH;
+  BwdArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.lse = lse;
+  a.dout = dout;
+  a.dq = dq;
+  a.dk = dk;
+  a.dv = dv;
+  a.delta = delta;  // every row is written by the Delta kernel before it is read
   return bwd_stages(p, a, kStageDelta | kStageDkdv | kStageDq, static_cast<hipStream_t>(stream));
 }
 

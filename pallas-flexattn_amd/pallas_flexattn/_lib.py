@@ -58,7 +58,8 @@ class FaMaskBuild(ctypes.Structure):
     ]
 
 
-EXPORTED = ("fa_fwd", "fa_fwd_splitkv", "fa_fwd_splitkv_workspace_bytes", "fa_bwd", "fa_bwd_workspace_bytes", "fa_bwd_preprocess", "fa_bwd_dkdv", "fa_bwd_dq",
+EXPORTED = ("fa_fwd", "fa_fwd_splitkv", "fa_fwd_splitkv_workspace_bytes", "fa_bwd", "fa_bwd_workspace_bytes",
+            "fa_bwd_noalloc", "fa_bwd_noalloc_max_rows", "fa_bwd_preprocess", "fa_bwd_dkdv", "fa_bwd_dq",
             "fa_mask_build_workspace_bytes", "fa_build_block_mask", "fa_strerror", "fa_abi_version")
 
 _lib = None
@@ -88,6 +89,10 @@ def load():
     lib.fa_fwd_splitkv_workspace_bytes.restype = ctypes.c_size_t
     lib.fa_bwd.argtypes = [P, v, v, v, v, v, v, v, v, v, v, ctypes.c_size_t, v]
     lib.fa_bwd.restype = ctypes.c_int
+    lib.fa_bwd_noalloc.argtypes = [P, v, v, v, v, v, v, v, v, v, v]
+    lib.fa_bwd_noalloc.restype = ctypes.c_int
+    lib.fa_bwd_noalloc_max_rows.argtypes = []
+    lib.fa_bwd_noalloc_max_rows.restype = ctypes.c_size_t
     lib.fa_bwd_preprocess.argtypes = [P, v, v, v, v]
     lib.fa_bwd_preprocess.restype = ctypes.c_int
     lib.fa_bwd_dkdv.argtypes = [P, v, v, v, v, v, v, v, v, v]

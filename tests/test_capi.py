@@ -28,7 +28,7 @@ def test_abi_version_and_strerror():
     lib = _lib.load()
     assert lib.fa_abi_version() == _lib.ABI_VERSION
     assert lib.fa_strerror(0) == b"success"
-    for code in range(-8, 0):
+    for code in range(-9, 0):
         assert lib.fa_strerror(code) != b"unknown status"
 
 
