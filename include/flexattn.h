@@ -51,7 +51,8 @@ enum fa_status {
   FA_ERR_WORKSPACE = -6,     /* workspace missing or too small */
   FA_ERR_LAUNCH = -7,        /* the HIP launch failed */
   FA_ERR_VERSION = -8,       /* params.abi_version != FA_ABI_VERSION */
-  FA_ERR_TOO_LARGE = -9      /* beyond the fixed scratch of fa_bwd_noalloc */
+  FA_ERR_TOO_LARGE = -9,     /* beyond the fixed scratch of fa_bwd_noalloc */
+  FA_ERR_COMPILE = -10       /* the run-time compile of user mods failed (see its log) */
 };
 
 /*
@@ -140,6 +141,53 @@ int fa_bwd(const fa_params *p, const void *q, const void *k, const void *v, cons
 size_t fa_bwd_noalloc_max_rows(void);
 int fa_bwd_noalloc(const fa_params *p, const void *q, const void *k, const void *v, const void *o,
                    const float *lse, const void *dout, void *dq, void *dk, void *dv, void *stream);
+
+/*
+ * User score / mask mods (the reference evaluates any mask_mod callable per
+ * element inside its kernels: flash_attn.py:85-88, :236-239, :341-344).  The
+ * forward, dQ and dK/dV kernels are compiled at run time (hipRTC) with a
+ * policy struct given as C++ source:
+ *
+ *   struct UserMod {
+ *     static constexpr bool kMask = ..., kScore = ...;
+ *     __device__ static bool mask(const fa::Problem& p, int b, int h, int q, int kv);
+ *     __device__ static float score(const fa::Problem& p, float s, int b, int h, int q, int kv, float* dsds);
+ *   };
+ *
+ * mask: whether (q, kv) attends, applied on partial tiles and dense walks
+ * (the block tables give the partial / full / skipped tiles, as for fa_fwd);
+ * score: the modified score of s = scale * q.k (natural units) and *dsds its
+ * derivative d score / d s, used by the backward.  Tensors the mods read are
+ * passed per call as `bufs` (up to 8 device pointers) and read in the policy
+ * through p.mod_buf[i].  The window / document fields of fa_params still
+ * apply; the built-in ALiBi / soft-cap apply when kScore is false (flag
+ * FA_MODS_BUILTIN_SCORE when they are set).
+ *
+ * fa_mods_compile (no GPU needed) returns a blob (malloc'd, release with
+ * fa_mods_free_blob) holding the code object; fa_mods_load loads it on the
+ * current GPU.  Kernel tiles are fixed: bf16 128 x 64 (forward, dQ) and
+ * 128 keys x 64 queries (dK/dV); float32 128 x 32.  The bf16 kernels take
+ * window / contiguous-document masks; document labels go into the user mask.
+ */
+enum fa_mods_flags { FA_MODS_MASK = 1, FA_MODS_SCORE = 2, FA_MODS_BUILTIN_SCORE = 4 };
+typedef struct fa_mods fa_mods;
+int fa_mods_compile(const char *policy_source, int dtype, int D, int flags, void **blob, size_t *blob_bytes,
+                    char *log, size_t log_bytes);
+void fa_mods_free_blob(void *blob);
+int fa_mods_load(const void *blob, size_t blob_bytes, fa_mods **out);
+int fa_mods_unload(fa_mods *m);
+int fa_mods_fwd(const fa_mods *m, const fa_params *p, const void *const *bufs, int nbufs, const void *q,
+                const void *k, const void *v, void *o, float *lse, void *stream);
+int fa_mods_bwd(const fa_mods *m, const fa_params *p, const void *const *bufs, int nbufs, const void *q,
+                const void *k, const void *v, const void *o, const float *lse, const void *dout, void *dq,
+                void *dk, void *dv, void *workspace, size_t workspace_bytes, void *stream);
+/* fa_bwd_dkdv / fa_bwd_dq with user mods (the Delta stage, fa_bwd_preprocess, does not depend on them) */
+int fa_mods_bwd_dkdv(const fa_mods *m, const fa_params *p, const void *const *bufs, int nbufs, const void *q,
+                     const void *k, const void *v, const void *dout, const float *lse, const float *delta, void *dk,
+                     void *dv, void *stream);
+int fa_mods_bwd_dq(const fa_mods *m, const fa_params *p, const void *const *bufs, int nbufs, const void *q,
+                   const void *k, const void *v, const void *dout, const float *lse, const float *delta, void *dq,
+                   void *stream);
 
 /* The three stages fa_bwd runs, callable one at a time (the reference exposes
  * the same split as flash_attention_bwd_preprocess / _dkv / _dq).

@@ -25,17 +25,19 @@ def _as64(x):
     return np.asarray(x, dtype=np.float64)
 
 
-def _scores(qh, kh, scale, h, Hq, alibi_slopes, softcap):
-    """Return (s_final, tanh_term or None) for one head, float64 (Sq, Skv)."""
+def _scores(qh, kh, scale, h, Hq, alibi_slopes, softcap, score_fn=None, b=0):
+    """Return (s_final, d s_final / d s or None) for one head, float64 (Sq, Skv)."""
     s = (qh @ kh.T) * scale
     sq, skv = s.shape
+    if score_fn is not None:
+        return score_fn(s, b, h, np.arange(sq)[:, None], np.arange(skv)[None, :])
     if alibi_slopes is not None:
         s = s + float(alibi_slopes[h]) * (np.arange(skv)[None, :] - np.arange(sq)[:, None]).astype(np.float64)
     th = None
     if softcap is not None and softcap > 0:
         th = np.tanh(s / softcap)
         s = softcap * th
-    return s, th
+    return s, (None if th is None else 1.0 - th * th)
 
 
 def _mask_for(mask, b, h, sq, skv):
@@ -60,11 +62,13 @@ def _softmax_rows(s):
     return p, lse
 
 
-def forward(q, k, v, mask=None, scale=None, alibi_slopes=None, softcap=None):
+def forward(q, k, v, mask=None, scale=None, alibi_slopes=None, softcap=None, score_fn=None):
     """q (B,Hq,Sq,D), k/v (B,Hkv,Skv,D) -> (o float64 (B,Hq,Sq,D), lse float64 (B,Hq,Sq)).
 
     ``mask`` is None, a boolean array (Sq,Skv) or (B|1,H|1,Sq,Skv), or a
-    callable ``mask(b, h, q_idx, kv_idx) -> bool``.
+    callable ``mask(b, h, q_idx, kv_idx) -> bool``.  ``score_fn(s, b, h,
+    q_idx, kv_idx) -> (s', d s' / d s)`` (float64 arrays) replaces ALiBi /
+    soft-cap with an arbitrary score modification of s = scale * q.k.
     """
     q, k, v = _as64(q), _as64(k), _as64(v)
     B, Hq, Sq, D = q.shape
@@ -75,7 +79,7 @@ def forward(q, k, v, mask=None, scale=None, alibi_slopes=None, softcap=None):
     lse = np.zeros((B, Hq, Sq))
     for b in range(B):
         for h in range(Hq):
-            s, _ = _scores(q[b, h], k[b, h // g], scale, h, Hq, alibi_slopes, softcap)
+            s, _ = _scores(q[b, h], k[b, h // g], scale, h, Hq, alibi_slopes, softcap, score_fn, b)
             m = _mask_for(mask, b, h, Sq, Skv)
             if m is not None:
                 s = np.where(m, s, -np.inf)
@@ -84,7 +88,7 @@ def forward(q, k, v, mask=None, scale=None, alibi_slopes=None, softcap=None):
     return o, lse
 
 
-def backward(q, k, v, do, mask=None, scale=None, alibi_slopes=None, softcap=None):
+def backward(q, k, v, do, mask=None, scale=None, alibi_slopes=None, softcap=None, score_fn=None):
     """Gradients of sum(forward(q,k,v) * do) w.r.t. q, k, v (float64)."""
     q, k, v, do = _as64(q), _as64(k), _as64(v), _as64(do)
     B, Hq, Sq, D = q.shape
@@ -97,7 +101,7 @@ def backward(q, k, v, do, mask=None, scale=None, alibi_slopes=None, softcap=None
     for b in range(B):
         for h in range(Hq):
             kh, vh = k[b, h // g], v[b, h // g]
-            s, th = _scores(q[b, h], kh, scale, h, Hq, alibi_slopes, softcap)
+            s, dsds = _scores(q[b, h], kh, scale, h, Hq, alibi_slopes, softcap, score_fn, b)
             m = _mask_for(mask, b, h, Sq, Skv)
             if m is not None:
                 s = np.where(m, s, -np.inf)
@@ -107,8 +111,8 @@ def backward(q, k, v, do, mask=None, scale=None, alibi_slopes=None, softcap=None
             dp = do[b, h] @ vh.T
             delta = np.sum(o * do[b, h], axis=-1, keepdims=True)
             ds = p * (dp - delta)
-            if th is not None:
-                ds = ds * (1.0 - th * th)
+            if dsds is not None:
+                ds = np.where(p > 0, ds * dsds, 0.0)
             ds = ds * scale
             dq[b, h] = ds @ kh
             dk[b, h // g] += ds.T @ q[b, h]

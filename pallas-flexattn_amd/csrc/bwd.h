@@ -167,7 +167,7 @@ struct QWalk {
 };
 
 // ----------------------------------------------------------------- dK dV ---
-template <typename T, int D, int BQ, int NW, bool kMods>
+template <typename T, int D, int BQ, int NW, bool kMods, class Mod = BuiltinMod>
 __global__ __launch_bounds__(NW * 64) void dkdv_kernel(BwdArgs a) {
   using E = Elt<T>;
   using frag = typename E::frag;
@@ -325,9 +325,9 @@ __global__ __launch_bounds__(NW * 64) void dkdv_kernel(BwdArgs a) {
           const int e = 4 * e4 + i;
           const int qi = qbase + r0 + i;
           float dsdx;
-          float t = score_t<kMods>(P, sacc[j][e], slope, qi, kw, &dsdx);
+          float t = mod_score_t<Mod, kMods>(P, sacc[j][e], slope, b, hq, qi, kw, &dsdx);
           if (masked) {
-            const bool ok = kvalid && qi < P.Sq && mask_ok(P, qi, kw, q_doc_of(P, b, qi), kdoc);
+            const bool ok = kvalid && qi < P.Sq && mod_mask_ok<Mod>(P, b, hq, qi, kw, q_doc_of(P, b, qi), kdoc);
             if (!ok) t = -INFINITY;
           }
           const float pv = fast_exp2(t - ls[i]);
@@ -382,7 +382,7 @@ __global__ __launch_bounds__(NW * 64) void dkdv_kernel(BwdArgs a) {
 }
 
 // -------------------------------------------------------------------- dQ ---
-template <typename T, int D, int BN, int NW, bool kMods>
+template <typename T, int D, int BN, int NW, bool kMods, class Mod = BuiltinMod>
 __global__ __launch_bounds__(NW * 64) void dq_kernel(BwdArgs a) {
   using E = Elt<T>;
   using frag = typename E::frag;
@@ -531,8 +531,8 @@ __global__ __launch_bounds__(NW * 64) void dq_kernel(BwdArgs a) {
       for (int e = 0; e < 16; ++e) {
         const int key = kbase + 32 * j + acc_row(e, hh);
         float dsdx;
-        float t = score_t<kMods>(P, sacc[j][e], slope, qw, key, &dsdx);
-        if (masked && !(key < P.Skv && mask_ok(P, qw, key, qdoc, kv_doc_of(P, b, key)))) t = -INFINITY;
+        float t = mod_score_t<Mod, kMods>(P, sacc[j][e], slope, b, h, qw, key, &dsdx);
+        if (masked && !(key < P.Skv && mod_mask_ok<Mod>(P, b, h, qw, key, qdoc, kv_doc_of(P, b, key)))) t = -INFINITY;
         const float pv = fast_exp2(t - lse2);
         pacc[j][e] = pv * (pacc[j][e] - dl) * dsdx;
       }

@@ -23,8 +23,6 @@
 // contiguous documents; other document layouts use the generic kernels);
 // full tiles skip it.
 #pragma once
-#include <type_traits>
-
 #include "bwd.h"
 #include "dma.h"
 
@@ -141,7 +139,7 @@ __device__ __forceinline__ void zero(f32x16& x) {
 }
 
 // ------------------------------------------------------------------- dQ ----
-template <int D, int BN, int NW, bool kMods>
+template <int D, int BN, int NW, bool kMods, class Mod = BuiltinMod>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(occupancy_for(4 * BN * D * 2, NW, 2))))
 void dq_bf16_kernel(BwdArgs a) {
   using E = Elt<uint16_t>;
@@ -248,14 +246,14 @@ void dq_bf16_kernel(BwdArgs a) {
       for (int e = 0; e < 16; ++e) {
         dsdx[e] = 1.f;
         if constexpr (kMods)
-          sacc[e] = score_mods_flat(sacc[e], P.scale, slope, qw, kbase + 32 * j + acc_row(e, hh), P.softcap, cap_inv,
+          sacc[e] = mod_score_flat<Mod>(P, sacc[e], slope, b, h, qw, kbase + 32 * j + acc_row(e, hh), cap_inv,
                                     &dsdx[e]);
       }
       if constexpr (kMasked) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int key = kbase + 32 * j + acc_row(e, hh);
-          sacc[e] = (key >= klo && key <= khi) ? sacc[e] : -INFINITY;
+          sacc[e] = mod_keep<Mod>(P, b, h, qw, key, klo, khi) ? sacc[e] : -INFINITY;
         }
       }
 #pragma unroll
@@ -315,8 +313,8 @@ void dq_bf16_kernel(BwdArgs a) {
   };
   const int n_full = walk.count_full();
   int it = 0;
-  for (; it < n_full; ++it) step(it, std::false_type{});
-  for (; it < n_it; ++it) step(it, std::true_type{});
+  for (; it < n_full; ++it) step(it, False{});
+  for (; it < n_it; ++it) step(it, True{});
 
 #pragma unroll
   for (int i = 0; i < DT; ++i) mfma_drain<'v'>(dqa[i]);
@@ -327,7 +325,7 @@ void dq_bf16_kernel(BwdArgs a) {
 }
 
 // ---------------------------------------------------------------- dK dV ----
-template <int D, int BQ, int NW, bool kMods>
+template <int D, int BQ, int NW, bool kMods, class Mod = BuiltinMod>
 __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   using E = Elt<uint16_t>;
   using frag = E::frag;
@@ -464,7 +462,7 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   // the start).  Score mods, when present, are evaluated branch-free in the
   // exponential's stage.  sched_barrier fences keep
   // the compiler to this order.
-  auto tile_fast = [&](int qbase, float slope, const char* ql, const char* dl_, const float* lsel,
+  auto tile_fast = [&](int qbase, int hq, float slope, const char* ql, const char* dl_, const float* lsel,
                        const float* dltl, auto&& copy_k, auto&& stat_k, auto masked_c) {
     constexpr bool kMasked = decltype(masked_c)::value;
     constexpr int KS = KSTEPS, NSTEP = 4 * KS, PF = APF, R = PF + 1;
@@ -483,6 +481,15 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
         const uint32_t up = 0xffffffffu >> (31 - max(hi, 0));
         const uint32_t dn = 0xffffffffu << min(lo, 31);
         rmask[j] = (hi >= lo) ? (up & dn) : 0u;
+        if constexpr (Mod::kMask) {  // user mask on the rows this lane holds
+          uint32_t bits = 0u;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int r = acc_row(e, 0);
+            bits |= Mod::mask(P, b, hq, base + r, kw) ? (1u << r) : 0u;
+          }
+          rmask[j] &= bits;
+        }
       }
     }
     // 0xffff / 0 halves for the two elements of pair p (rows r, r + 1)
@@ -537,8 +544,8 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
         const int e = 2 * p + i, q = e >> 2;
         if constexpr (kMods) {
           // score mods (log2-domain logit) and d s / d(scale q.k) for dS
-          const float t = score_mods_flat(sacc[j][e], P.scale, slope, qbase + 32 * j + acc_row(e, hh), kw,
-                                          P.softcap, cap_inv, &dsq[p][i]);
+          const float t = mod_score_flat<Mod>(P, sacc[j][e], slope, b, hq, qbase + 32 * j + acc_row(e, hh), kw,
+                                              cap_inv, &dsq[p][i]);
           pvq[p][i] = fast_exp2(t + ls[j][q][e & 3]);
         } else {
           pvq[p][i] = fast_exp2(fmaf(sacc[j][e], P.scale_log2, ls[j][q][e & 3]));
@@ -656,7 +663,7 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
     auto fetch_next = [&]() { ref_next = walk.fetch(min(it + 2, n_it - 1)); };
     if (qbase < P.Sq) {
       const float slope = (kMods && P.alibi) ? P.alibi[hq] : 0.f;
-      tile_fast(qbase, slope, lds + buf * TILE, lds + (2 + buf) * TILE,
+      tile_fast(qbase, hq, slope, lds + buf * TILE, lds + (2 + buf) * TILE,
                 reinterpret_cast<const float*>(lds + 4 * TILE + buf * STAT),
                 reinterpret_cast<const float*>(lds + 4 * TILE + (2 + buf) * STAT), copy_k, stat_k, masked_c);
       fetch_next();
@@ -671,8 +678,8 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   };
   const int n_full = walk.count_full();
   int it = 0;
-  for (; it < n_full; ++it) step(it, std::false_type{});
-  for (; it < n_it; ++it) step(it, std::true_type{});
+  for (; it < n_full; ++it) step(it, False{});
+  for (; it < n_it; ++it) step(it, True{});
 
 #pragma unroll
   for (int i = 0; i < DT; ++i) {

@@ -1,15 +1,28 @@
 // C ABI of libflexattn.so: argument validation, tile-config selection and
 // kernel launches.  See include/flexattn.h for the contract.
 #include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
 
+#include <cstdlib>
+#include <cstring>
 #include <initializer_list>
 #include <mutex>
+#include <string>
+#include <vector>
 
 #include "../../include/flexattn.h"
 #include "bwd.h"
 #include "bwd_bf16.h"
 #include "fwd_bf16.h"
 #include "mask_build.h"
+
+// Kernels compiled at run time for one set of user mods (user_mods.h),
+// loaded on one GPU.
+struct fa_mods {
+  hipModule_t module = nullptr;
+  hipFunction_t fwd = nullptr, dq = nullptr, dkdv = nullptr;
+  int dtype = 0, D = 0, flags = 0, device = -1;
+};
 
 namespace {
 
@@ -337,6 +350,8 @@ size_t split_bytes(const fa_params* p, int n) {
   return n > 1 ? (size_t)n * p->B * p->Hq * p->Sq * (p->D + 2) * sizeof(float) : 0;
 }
 
+#include "user_mods.h"
+
 }  // namespace
 
 extern "C" {
@@ -355,6 +370,7 @@ const char* fa_strerror(int status) {
     case FA_ERR_LAUNCH: return "HIP kernel launch failed";
     case FA_ERR_VERSION: return "fa_params.abi_version does not match the library";
     case FA_ERR_TOO_LARGE: return "B * Hq * Sq exceeds fa_bwd_noalloc_max_rows()";
+    case FA_ERR_COMPILE: return "the run-time compile of the user mods failed (see the compile log)";
     default: return "unknown status";
   }
 }
@@ -517,6 +533,148 @@ int fa_bwd_dq(const fa_params* p, const void* q, const void* k, const void* v, c
   a.delta = const_cast<float*>(delta);
   a.dq = dq;
   return bwd_stages(p, a, kStageDq, static_cast<hipStream_t>(stream));
+}
+
+int fa_mods_compile(const char* policy_source, int dtype, int D, int flags, void** blob, size_t* blob_bytes,
+                    char* log, size_t log_bytes) {
+  if (!blob || !blob_bytes) return FA_ERR_NULL;
+  std::vector<char> b;
+  const int rc = compile_mods(policy_source, dtype, D, flags, &b, log, log_bytes);
+  if (rc) return rc;
+  void* mem = malloc(b.size());
+  if (!mem) return FA_ERR_NULL;
+  memcpy(mem, b.data(), b.size());
+  *blob = mem;
+  *blob_bytes = b.size();
+  return FA_OK;
+}
+
+void fa_mods_free_blob(void* blob) { free(blob); }
+
+int fa_mods_load(const void* blob, size_t blob_bytes, fa_mods** out) { return load_mods(blob, blob_bytes, out); }
+
+int fa_mods_unload(fa_mods* m) {
+  if (!m) return FA_ERR_NULL;
+  const int rc = hipModuleUnload(m->module) == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
+  delete m;
+  return rc;
+}
+
+int fa_mods_fwd(const fa_mods* m, const fa_params* p, const void* const* bufs, int nbufs, const void* q,
+                const void* k, const void* v, void* o, float* lse, void* stream) {
+  FwdArgs a;
+  Tiles t;
+  int rc = mods_problem(m, p, bufs, nbufs, &a.p, &t);
+  if (rc) return rc;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev != m->device) return FA_ERR_LAUNCH;
+  if (!q || !k || !v || !o || !lse) return FA_ERR_NULL;
+  if (!aligned16({q, k, v, o})) return FA_ERR_SHAPE;
+  if (a.p.has_tables && (a.p.mblk_q % t.bm || a.p.mblk_kv % t.bn)) return FA_ERR_TABLES;
+  if (a.p.has_tables && !a.p.kv_num && !a.p.full_kv_num) return FA_ERR_TABLES;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.lse = lse;
+  const unsigned grid = (unsigned)(a.p.B * a.p.Hq * cdiv(a.p.Sq, t.bm));
+  return launch_module(m->fwd, grid, 256, a, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"
+
+namespace {
+
+// The backward stages with user mods: Delta (the library's own kernel), dK/dV
+// and dQ (the run-time compiled ones).
+int mods_bwd_stages(const fa_mods* m, const fa_params* p, const void* const* bufs, int nbufs, BwdArgs& a,
+                    int stages, hipStream_t s) {
+  Tiles t;
+  int rc = mods_problem(m, p, bufs, nbufs, &a.p, &t);
+  if (rc) return rc;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev != m->device) return FA_ERR_LAUNCH;
+  if (a.p.has_tables && (stages & (kStageDkdv | kStageDq))) {
+    if (a.p.mblk_q % t.bm || a.p.mblk_kv % t.bn || a.p.mblk_kv % t.bkv || a.p.mblk_q % t.bq) return FA_ERR_TABLES;
+    if ((stages & kStageDq) && !a.p.kv_num && !a.p.full_kv_num) return FA_ERR_TABLES;
+    if ((stages & kStageDkdv) && !a.p.q_num && !a.p.full_q_num) return FA_ERR_TABLES;
+  }
+  if (stages & kStageDelta) {
+    if (p->dtype == FA_DTYPE_BF16)
+      rc = p->D == 32 ? run_delta<uint16_t, 32>(a, s) : p->D == 64 ? run_delta<uint16_t, 64>(a, s)
+                                                                    : run_delta<uint16_t, 128>(a, s);
+    else
+      rc = p->D == 32 ? run_delta<float, 32>(a, s) : p->D == 64 ? run_delta<float, 64>(a, s)
+                                                                 : run_delta<float, 128>(a, s);
+    if (rc) return rc;
+  }
+  if (stages & kStageDkdv) {
+    rc = launch_module(m->dkdv, (unsigned)(a.p.B * a.p.Hkv * cdiv(a.p.Skv, t.bkv)), 256, a, s);
+    if (rc) return rc;
+  }
+  if (stages & kStageDq) rc = launch_module(m->dq, (unsigned)(a.p.B * a.p.Hq * cdiv(a.p.Sq, t.bm)), 256, a, s);
+  return rc;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fa_mods_bwd(const fa_mods* m, const fa_params* p, const void* const* bufs, int nbufs, const void* q,
+                const void* k, const void* v, const void* o, const float* lse, const void* dout, void* dq,
+                void* dk, void* dv, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!m || !p) return FA_ERR_NULL;
+  if (!q || !k || !v || !o || !lse || !dout || !dq || !dk || !dv) return FA_ERR_NULL;
+  if (!aligned16({q, k, v, o, dout, dq, dk, dv})) return FA_ERR_SHAPE;
+  if (!workspace || workspace_bytes < delta_bytes(p)) return FA_ERR_WORKSPACE;
+  BwdArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.lse = lse;
+  a.dout = dout;
+  a.dq = dq;
+  a.dk = dk;
+  a.dv = dv;
+  a.delta = static_cast<float*>(workspace);
+  return mods_bwd_stages(m, p, bufs, nbufs, a, kStageDelta | kStageDkdv | kStageDq,
+                         static_cast<hipStream_t>(stream));
+}
+
+int fa_mods_bwd_dkdv(const fa_mods* m, const fa_params* p, const void* const* bufs, int nbufs, const void* q,
+                     const void* k, const void* v, const void* dout, const float* lse, const float* delta, void* dk,
+                     void* dv, void* stream) {
+  if (!m || !p) return FA_ERR_NULL;
+  if (!q || !k || !v || !dout || !lse || !delta || !dk || !dv) return FA_ERR_NULL;
+  if (!aligned16({q, k, v, dout, dk, dv})) return FA_ERR_SHAPE;
+  BwdArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.dout = dout;
+  a.lse = lse;
+  a.delta = const_cast<float*>(delta);
+  a.dk = dk;
+  a.dv = dv;
+  return mods_bwd_stages(m, p, bufs, nbufs, a, kStageDkdv, static_cast<hipStream_t>(stream));
+}
+
+int fa_mods_bwd_dq(const fa_mods* m, const fa_params* p, const void* const* bufs, int nbufs, const void* q,
+                   const void* k, const void* v, const void* dout, const float* lse, const float* delta, void* dq,
+                   void* stream) {
+  if (!m || !p) return FA_ERR_NULL;
+  if (!q || !k || !v || !dout || !lse || !delta || !dq) return FA_ERR_NULL;
+  if (!aligned16({q, k, v, dout, dq})) return FA_ERR_SHAPE;
+  BwdArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.dout = dout;
+  a.lse = lse;
+  a.delta = const_cast<float*>(delta);
+  a.dq = dq;
+  return mods_bwd_stages(m, p, bufs, nbufs, a, kStageDq, static_cast<hipStream_t>(stream));
 }
 
 size_t fa_mask_build_workspace_bytes(const fa_mask_build* m) {

@@ -15,10 +15,37 @@
 // therefore feed the next MFMA directly as a B (or A) operand with eight
 // consecutive k per lane half — no LDS round trip for P or dS.
 #pragma once
+// hipRTC (the run-time compiler that builds kernels with user score / mask
+// mods from these same headers) provides the HIP runtime and the integer
+// types itself and has no system headers.
+#ifndef __HIPCC_RTC__
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#else
+using __hip_internal::int16_t;
+using __hip_internal::int32_t;
+using __hip_internal::int64_t;
+using __hip_internal::uint16_t;
+using __hip_internal::uint32_t;
+using __hip_internal::uint64_t;
+using __hip_internal::uint8_t;
+typedef __hip_internal::uint64_t uintptr_t;
+typedef __SIZE_TYPE__ size_t;
+#endif
+#ifndef INFINITY
+#define INFINITY __builtin_inff()
+#endif
 
 namespace fa {
+
+// compile-time booleans used as tag arguments (std::integral_constant without
+// <type_traits>, which hipRTC lacks)
+template <bool B>
+struct Bool {
+  static constexpr bool value = B;
+};
+using False = Bool<false>;
+using True = Bool<true>;
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));

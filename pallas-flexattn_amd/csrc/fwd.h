@@ -84,7 +84,7 @@ struct KvWalk {
   }
 };
 
-template <typename T, int D, int BN, int NW, bool kMods>
+template <typename T, int D, int BN, int NW, bool kMods, class Mod = BuiltinMod>
 __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdArgs a) {
   using E = Elt<T>;
   using frag = typename E::frag;
@@ -229,8 +229,8 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdArgs a) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int key = kbase + 32 * j + acc_row(e, hh);
-        float t = score_t<kMods>(P, sacc[j][e], slope, qw, key, nullptr);
-        if (masked && !(key < P.Skv && mask_ok(P, qw, key, qdoc, kv_doc_of(P, b, key)))) t = -INFINITY;
+        float t = mod_score_t<Mod, kMods>(P, sacc[j][e], slope, b, h, qw, key, nullptr);
+        if (masked && !(key < P.Skv && mod_mask_ok<Mod>(P, b, h, qw, key, qdoc, kv_doc_of(P, b, key)))) t = -INFINITY;
         sacc[j][e] = t;
         mx = fmaxf(mx, t);
       }

@@ -23,8 +23,6 @@
 // slots; V chunk c sits in slot c ^ tr_swz(r) — the 4 consecutive rows of one
 // transposing read land in distinct quarter-rows.
 #pragma once
-#include <type_traits>
-
 #include "dma.h"
 #include "fwd.h"
 
@@ -37,7 +35,7 @@
 
 namespace fa {
 
-template <int D, int BN, int NW, bool kMods>
+template <int D, int BN, int NW, bool kMods, class Mod = BuiltinMod>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(occupancy_for(4 * BN * D * 2, NW, 2))))
 void fwd_bf16_kernel(FwdArgs a) {
   using E = Elt<uint16_t>;
@@ -290,8 +288,8 @@ void fwd_bf16_kernel(FwdArgs a) {
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             float dsdx;  // unused in the forward
-            sacc[j][e] = score_mods_flat(sacc[j][e], P.scale, slope, qw, kbase + 32 * j + acc_row(e, hh), P.softcap,
-                                         cap_inv, &dsdx);
+            sacc[j][e] = mod_score_flat<Mod>(P, sacc[j][e], slope, b, h, qw, kbase + 32 * j + acc_row(e, hh), cap_inv,
+                                             &dsdx);
           }
       }
       if (masked) {  // partial tile: keys outside [klo, khi] are dropped
@@ -300,7 +298,7 @@ void fwd_bf16_kernel(FwdArgs a) {
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             const int key = kbase + 32 * j + acc_row(e, hh);
-            sacc[j][e] = (key >= klo && key <= khi) ? sacc[j][e] : -INFINITY;
+            sacc[j][e] = mod_keep<Mod>(P, b, h, qw, key, klo, khi) ? sacc[j][e] : -INFINITY;
           }
       }
       // V^T fragments of d tile i (two tiles in flight): tile 0's reads issue

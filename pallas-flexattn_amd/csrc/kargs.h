@@ -35,6 +35,26 @@ struct Problem {
   int xcd_remap;         // group work of a head onto one XCD
   int head_group_q;      // heads per level-major group, q-tile walks (forward, dQ)
   int head_group_kv;     // the same for kv-tile walks (dK/dV)
+  // tensors read by user score / mask mods compiled at run time (see Mod below)
+  const void* mod_buf[8];
+};
+
+// Element policy of the kernels.  BuiltinMod: the element mask is the window
+// / document terms of the Problem and the score epilogue its ALiBi + soft-cap.
+// A policy compiled at run time from user mods (fa_mods_build) has the same
+// members with kMask / kScore set and
+//   static bool  mask(const Problem&, int b, int h, int q, int kv)
+//   static float score(const Problem&, float s, int b, int h, int q, int kv, float* dsds)
+// where s = scale * q.k, the result is the modified score (natural units)
+// and *dsds its derivative with respect to s.
+struct BuiltinMod {
+  static constexpr bool kMask = false;
+  static constexpr bool kScore = false;
+  __device__ static bool mask(const Problem&, int, int, int, int) { return true; }
+  __device__ static float score(const Problem&, float s, int, int, int, int, float* dsds) {
+    *dsds = 1.0f;
+    return s;
+  }
 };
 
 // Window part of the element mask (q, kv inside the sequence bounds).
@@ -123,6 +143,45 @@ __device__ __forceinline__ float score_mods_flat(float raw, float scale, float s
   *dsdx = capped ? fmaf(-th, th, 1.0f) : 1.0f;
   s = capped ? softcap * th : s;
   return s * kLog2e;
+}
+
+// Log2-domain logit of raw q.k under the policy: a user score mod, or the
+// built-in ALiBi + soft-cap epilogue (score_mods_flat).
+template <class Mod>
+__device__ __forceinline__ float mod_score_flat(const Problem& P, float raw, float slope, int b, int h, int q, int k,
+                                                float cap_inv, float* dsdx) {
+  if constexpr (Mod::kScore) return Mod::score(P, raw * P.scale, b, h, q, k, dsdx) * kLog2e;
+  else return score_mods_flat(raw, P.scale, slope, q, k, P.softcap, cap_inv, dsdx);
+}
+
+// score_t under the policy (generic kernels).
+template <class Mod, bool kMods>
+__device__ __forceinline__ float mod_score_t(const Problem& P, float raw, float slope, int b, int h, int q, int k,
+                                             float* dsdx) {
+  if constexpr (Mod::kScore) {
+    float d;
+    const float t = Mod::score(P, raw * P.scale, b, h, q, k, &d) * kLog2e;
+    if (dsdx) *dsdx = d;
+    return t;
+  } else {
+    return score_t<kMods>(P, raw, slope, q, k, dsdx);
+  }
+}
+
+// Element (q, k) of a partial tile is kept: inside [lo, hi] (the interval
+// of keys the window / contiguous documents leave to query q, which also
+// bounds k below Skv) and, with a user mask, where the mask holds.
+template <class Mod>
+__device__ __forceinline__ bool mod_keep(const Problem& P, int b, int h, int q, int k, int lo, int hi) {
+  if constexpr (Mod::kMask) return k >= lo && k <= hi && Mod::mask(P, b, h, q, k);
+  else return k >= lo && k <= hi;
+}
+
+// mask_ok under the policy (generic kernels).
+template <class Mod>
+__device__ __forceinline__ bool mod_mask_ok(const Problem& P, int b, int h, int q, int k, int qdoc, int kdoc) {
+  if constexpr (Mod::kMask) return mask_ok(P, q, k, qdoc, kdoc) && Mod::mask(P, b, h, q, k);
+  else return mask_ok(P, q, k, qdoc, kdoc);
 }
 
 // Tile start used for out-of-range table entries: beyond any sequence, so the

@@ -60,7 +60,11 @@ class FaMaskBuild(ctypes.Structure):
 
 EXPORTED = ("fa_fwd", "fa_fwd_splitkv", "fa_fwd_splitkv_workspace_bytes", "fa_bwd", "fa_bwd_workspace_bytes",
             "fa_bwd_noalloc", "fa_bwd_noalloc_max_rows", "fa_bwd_preprocess", "fa_bwd_dkdv", "fa_bwd_dq",
-            "fa_mask_build_workspace_bytes", "fa_build_block_mask", "fa_strerror", "fa_abi_version")
+            "fa_mask_build_workspace_bytes", "fa_build_block_mask", "fa_strerror", "fa_abi_version",
+            "fa_mods_compile", "fa_mods_free_blob", "fa_mods_load", "fa_mods_unload", "fa_mods_fwd", "fa_mods_bwd",
+            "fa_mods_bwd_dkdv", "fa_mods_bwd_dq")
+
+MODS_MASK, MODS_SCORE, MODS_BUILTIN_SCORE = 1, 2, 4
 
 _lib = None
 
@@ -106,6 +110,24 @@ def load():
     lib.fa_mask_build_workspace_bytes.restype = ctypes.c_size_t
     lib.fa_build_block_mask.argtypes = [M, v, ctypes.c_size_t, v]
     lib.fa_build_block_mask.restype = ctypes.c_int
+    i = ctypes.c_int
+    lib.fa_mods_compile.argtypes = [ctypes.c_char_p, i, i, i, ctypes.POINTER(v), ctypes.POINTER(ctypes.c_size_t),
+                                    ctypes.c_char_p, ctypes.c_size_t]
+    lib.fa_mods_compile.restype = i
+    lib.fa_mods_free_blob.argtypes = [v]
+    lib.fa_mods_free_blob.restype = None
+    lib.fa_mods_load.argtypes = [v, ctypes.c_size_t, ctypes.POINTER(v)]
+    lib.fa_mods_load.restype = i
+    lib.fa_mods_unload.argtypes = [v]
+    lib.fa_mods_unload.restype = i
+    lib.fa_mods_fwd.argtypes = [v, P, v, i, v, v, v, v, v, v]
+    lib.fa_mods_fwd.restype = i
+    lib.fa_mods_bwd.argtypes = [v, P, v, i, v, v, v, v, v, v, v, v, v, v, ctypes.c_size_t, v]
+    lib.fa_mods_bwd.restype = i
+    lib.fa_mods_bwd_dkdv.argtypes = [v, P, v, i, v, v, v, v, v, v, v, v, v]
+    lib.fa_mods_bwd_dkdv.restype = i
+    lib.fa_mods_bwd_dq.argtypes = [v, P, v, i, v, v, v, v, v, v, v, v]
+    lib.fa_mods_bwd_dq.restype = i
     lib.fa_strerror.argtypes = [ctypes.c_int]
     lib.fa_strerror.restype = ctypes.c_char_p
     lib.fa_abi_version.argtypes = []
@@ -120,3 +142,53 @@ def check(status: int) -> None:
     if status != 0:
         msg = load().fa_strerror(status).decode()
         raise FlexAttnError(f"flexattn C ABI error {status}: {msg}")
+
+
+# Runs fa_mods_compile in a fresh interpreter.  torch ships its own copies of
+# the HIP runtime, hipRTC and comgr (an older LLVM than the one libflexattn.so
+# is built with); once torch is imported those copies serve the whole
+# process, so an in-process compile would use a different compiler than the
+# library's own kernels (and reject the library's compile options).  The child
+# loads only libflexattn.so and the ROCm libraries it was linked against.
+_CHILD = r"""
+import ctypes, sys
+lib = ctypes.CDLL(sys.argv[1])
+lib.fa_mods_compile.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_size_t),
+                                ctypes.c_char_p, ctypes.c_size_t]
+lib.fa_mods_free_blob.argtypes = [ctypes.c_void_p]
+src = sys.stdin.buffer.read()
+blob, size = ctypes.c_void_p(), ctypes.c_size_t()
+log = ctypes.create_string_buffer(1 << 16)
+rc = lib.fa_mods_compile(src, int(sys.argv[2]), int(sys.argv[3]), int(sys.argv[4]), ctypes.byref(blob),
+                         ctypes.byref(size), log, len(log))
+sys.stderr.write(log.value.decode(errors="replace"))
+if rc == 0:
+    with open(sys.argv[5], "wb") as f:
+        f.write(ctypes.string_at(blob, size.value))
+    lib.fa_mods_free_blob(blob)
+sys.exit(0 if rc == 0 else 3)
+"""
+
+
+def compile_mods(source: str, dtype: int, head_dim: int, flags: int) -> bytes:
+    """Compile a user-mods policy (C ABI fa_mods_compile, no GPU needed) in a
+    child interpreter and return the code blob.  Raises FlexAttnError with
+    the compiler log."""
+    import subprocess
+    import sys
+    import tempfile
+    if not os.path.exists(LIB_PATH):
+        load()  # raises the missing-library error
+    fd, out = tempfile.mkstemp(suffix=".blob")
+    os.close(fd)
+    try:
+        res = subprocess.run([sys.executable, "-c", _CHILD, LIB_PATH, str(dtype), str(head_dim), str(flags), out],
+                             input=source.encode(), capture_output=True, timeout=600)
+        if res.returncode != 0:
+            raise FlexAttnError(f"compiling the user mods failed (exit {res.returncode}):\n"
+                                f"{res.stderr.decode(errors='replace')[-8000:]}\n--- policy source ---\n{source}")
+        with open(out, "rb") as f:
+            return f.read()
+    finally:
+        os.unlink(out)

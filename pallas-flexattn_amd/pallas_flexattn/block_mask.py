@@ -25,6 +25,7 @@ import warnings
 
 import numpy as np
 
+from .lowering import LoweredMask, LoweringError, lower_mask
 from .mask_mod import MaskMod, MaskSpec
 
 
@@ -101,6 +102,8 @@ class BlockMask:
 def _arity(fn) -> int:
     if isinstance(fn, MaskSpec):
         return 2
+    if isinstance(fn, LoweredMask):
+        return 4
     try:
         params = [p for p in inspect.signature(fn).parameters.values()
                   if p.kind in (p.POSITIONAL_ONLY, p.POSITIONAL_OR_KEYWORD, p.VAR_POSITIONAL)]
@@ -121,6 +124,8 @@ def _mask_dims(mask_mod, B: int, H: int) -> Tuple[int, int]:
     """(TB, TH): how many distinct table rows the mask needs."""
     if isinstance(mask_mod, MaskSpec):
         return (mask_mod.doc_ids.shape[0] if mask_mod.batch_dependent else 1), 1
+    if isinstance(mask_mod, LoweredMask):  # tables per (b, h) for (b, h, q_idx, kv_idx) callables
+        return (B, H) if mask_mod.arity == 4 else (1, 1)
     if _arity(mask_mod) == 4:
         return B, H
     return 1, 1
@@ -346,6 +351,14 @@ def create_block_mask(
     exact tables).  With ``device`` (a GPU) and a mask descriptor
     (:class:`MaskSpec`), both are evaluated on the device by the HIP
     library, with identical results, and the tables stay cached there."""
+    if not isinstance(mask_mod, (MaskSpec, LoweredMask)) and callable(mask_mod):
+        # a callable is traced once: the tables come from the expression the
+        # kernels will evaluate (callables that cannot be traced are called
+        # directly on numpy index arrays)
+        try:
+            mask_mod = lower_mask(mask_mod)
+        except LoweringError:
+            pass
     if device is not None and isinstance(mask_mod, MaskSpec):
         num, col, tables, dev_tables = _build_on_device(mask_mod, Q_LEN, KV_LEN, block_size, device)
         if num.shape[0] == 1:

@@ -22,11 +22,12 @@ plus the FlexAttention front door :func:`flex_attention` (``score_mod``,
 reference; this build has no host execution path and raises.
 """
 import math
+import os
 from typing import Optional, Tuple
 
 import numpy as np
 
-from . import _lib
+from . import _lib, lowering
 from .block_mask import BlockMask, _finish, create_block_mask
 from .kernel_tuner import (DEFAULT_BLOCK_C, DEFAULT_BLOCK_R, DEFAULT_NUM_STAGES, DEFAULT_NUM_WARPS,
                            kernel_tiles, tuned_tiles)
@@ -181,24 +182,149 @@ def _internal_block_mask(mask: MaskSpec, B: int, Sq: int, Skv: int, device=None)
 
 
 def _as_mask_spec(mask_mod) -> Optional[MaskSpec]:
-    if mask_mod is None:
-        return None
-    if isinstance(mask_mod, MaskSpec):
-        return mask_mod
-    raise NotImplementedError(
-        "the MI355X kernels evaluate mask mods as fused epilogues: use causal_mask, bidirectional_mask, "
-        "sliding_window_mask, document_mask or and_masks of them (arbitrary callables work with "
-        "create_block_mask and mha_reference only)")
+    """The built-in descriptor of a mask mod (None for callables, which are lowered)."""
+    mask, _, _ = _resolve(mask_mod, None)
+    return mask
+
+
+_LOWERED = {}
+
+
+def _lowered(fn, kind):
+    """The traced form of a callable, cached per callable object."""
+    hit = _LOWERED.get((kind, id(fn)))
+    if hit is not None and hit[0] is fn:
+        return hit[1]
+    try:
+        low = lowering.lower_mask(fn) if kind == "mask" else lowering.lower_score(fn)
+    except lowering.LoweringError as e:
+        raise NotImplementedError(f"this {kind}_mod cannot be lowered onto the MI355X kernels: {e}") from e
+    if len(_LOWERED) > 256:
+        _LOWERED.clear()
+    _LOWERED[(kind, id(fn))] = (fn, low)
+    return low
+
+
+_MODS = {}
+
+
+def _resolve(mask_mod, score_mod):
+    """(mask descriptor, score descriptor, user mods) for a call.  Built-in
+    descriptors (MaskSpec, ScoreSpec) run as the kernels' fused epilogues;
+    any other callable is traced and lowered onto the kernels (run-time
+    compiled element policy).  A document-label mask next to a user score mod
+    is lowered too (the bf16 tile kernels take documents only as intervals)."""
+    mask = score = None
+    lmask = lscore = None
+    if mask_mod is not None:
+        if isinstance(mask_mod, MaskSpec):
+            mask = mask_mod
+        else:
+            lmask = _lowered(mask_mod, "mask")
+            if lmask.is_trivial:
+                lmask = None
+    if score_mod is not None:
+        if isinstance(score_mod, ScoreSpec):
+            score = None if (score_mod.alibi is None and score_mod.softcap == 0) else score_mod
+        else:
+            lscore = _lowered(score_mod, "score")
+    if lscore is not None and mask is not None and mask.doc_ids is not None and mask.doc_bounds() is None:
+        lmask, mask = _lowered(mask, "mask"), None
+    if lmask is None and lscore is None:
+        return mask, score, None
+    key = (id(lmask), id(lscore))
+    hit = _MODS.get(key)
+    if hit is None or hit[0] is not lmask or hit[1] is not lscore:
+        if len(_MODS) > 256:
+            _MODS.clear()
+        hit = _MODS[key] = (lmask, lscore, lowering.UserMods(lmask, lscore))
+    return mask, score, hit[2]
 
 
 def _as_score_spec(score_mod) -> Optional[ScoreSpec]:
-    if score_mod is None:
-        return None
-    if isinstance(score_mod, ScoreSpec):
-        return None if (score_mod.alibi is None and score_mod.softcap == 0) else score_mod
-    raise NotImplementedError(
-        "the MI355X kernels support the fused score mods alibi_score_mod, softcap_score_mod and their "
-        "composition; arbitrary callables are not lowered")
+    _, score, _ = _resolve(None, score_mod)
+    return score
+
+
+_HANDLES = {}
+
+
+def _lib_identity():
+    """Identifies the library build (the run-time compiled kernels come from
+    its embedded headers): size and modification time of the .so."""
+    st = os.stat(_lib.LIB_PATH)
+    return f"{st.st_size}-{int(st.st_mtime)}"
+
+
+def _mods_handle(mods, dtype_code, D, flags, device):
+    """Loaded kernels (C ABI fa_mods) for a policy on a device: compiled once
+    per process, the code blob kept in a disk cache across processes
+    ($FLEXATTN_CACHE_DIR, default ~/.cache/pallas_flexattn)."""
+    import ctypes
+    import hashlib
+    dev = _torch().device(device)
+    idx = dev.index if dev.index is not None else _torch().cuda.current_device()
+    key = (mods.digest, dtype_code, D, flags, idx)
+    h = _HANDLES.get(key)
+    if h is not None:
+        return h
+    lib = _lib.load()
+    tag = hashlib.sha256(f"{mods.source}|{dtype_code}|{D}|{flags}|{_lib_identity()}".encode()).hexdigest()
+    cache_dir = os.environ.get("FLEXATTN_CACHE_DIR") or os.path.join(os.path.expanduser("~"), ".cache",
+                                                                     "pallas_flexattn")
+    path = os.path.join(cache_dir, f"mods-{tag}.blob")
+    blob = None
+    if os.path.exists(path):
+        with open(path, "rb") as f:
+            blob = f.read()
+    if blob is None:
+        blob = _lib.compile_mods(mods.source, dtype_code, D, flags)
+        try:
+            os.makedirs(cache_dir, exist_ok=True)
+            tmp = f"{path}.{os.getpid()}.tmp"
+            with open(tmp, "wb") as f:
+                f.write(blob)
+            os.replace(tmp, path)
+        except OSError:
+            pass  # the cache is an optimisation only
+    handle = ctypes.c_void_p()
+    with _torch().cuda.device(idx):
+        _lib.check(lib.fa_mods_load(blob, len(blob), ctypes.byref(handle)))
+    _HANDLES[key] = handle
+    return handle
+
+
+def _mods_args(mods, plan, q, score):
+    """(handle, buffer-pointer array, count) for a launch with user mods."""
+    import ctypes
+    bufs = mods.device_buffers(q.device)
+    arr = (ctypes.c_void_p * max(1, len(bufs)))(*[b.data_ptr() for b in bufs])
+    code, _ = _dtype_code(q)
+    flags = mods.flags(builtin_score=score is not None)
+    return _mods_handle(mods, code, q.shape[3], flags, q.device), arr, len(bufs)
+
+
+def _user_block_mask(lmask, B, H, Sq, Skv):
+    """Exact tables of a lowered mask at the kernels' table granularity
+    (evaluated on the host from the traced expression), cached."""
+    key = ("user", id(lmask), B, H, Sq, Skv)
+    hit = _MASK_CACHE.get(key)
+    if hit is None or hit[0] is not lmask:
+        if len(_MASK_CACHE) > 64:
+            _MASK_CACHE.clear()
+        hit = _MASK_CACHE[key] = (lmask, create_block_mask(lmask, B, H, Sq, Skv, TABLE_BLOCK))
+    return hit[1]
+
+
+def _tables_for(mask, mods, block_mask, q, k):
+    """The block mask a call walks: the caller's, or one built for its mask."""
+    if block_mask is not None:
+        return block_mask
+    if mask is not None and not mask.is_trivial:
+        return _internal_block_mask(mask, q.shape[0], q.shape[2], k.shape[2], q.device)
+    if mods is not None and mods.mask is not None:
+        return _user_block_mask(mods.mask, q.shape[0], q.shape[1], q.shape[2], k.shape[2])
+    return None
 
 
 def _stream():
@@ -211,25 +337,31 @@ def _dense16(t):
     return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
-def _fwd_core(q, k, v, mask, score, scale, block_mask, tiles):
-    """Forward through fa_fwd -> (o, lse fp32, plan)."""
+def _fwd_core(q, k, v, mask, score, scale, block_mask, tiles, mods=None):
+    """Forward through fa_fwd (fa_mods_fwd with user mods) -> (o, lse fp32, plan)."""
     torch = _torch()
     _check_inputs(q, k, v)
     q, k, v = _dense16(q), _dense16(k), _dense16(v)
-    if block_mask is None and mask is not None and not mask.is_trivial:
-        block_mask = _internal_block_mask(mask, q.shape[0], q.shape[2], k.shape[2], q.device)
+    block_mask = _tables_for(mask, mods, block_mask, q, k)
+    if mods is not None:
+        tiles = _MODS_TILES[_dtype_code(q)[1]]
     plan = _get_plan(q, k, mask, score, scale, block_mask, tiles)
     o = torch.empty_like(q)
     lse = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
     lib = _lib.load()
-    _lib.check(lib.fa_fwd(plan.ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
-                          _stream()))
+    ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr())
+    if mods is None:
+        _lib.check(lib.fa_fwd(plan.ptr(), *ptrs, _stream()))
+    else:
+        h, bufs, n = _mods_args(mods, plan, q, score)
+        _lib.check(lib.fa_mods_fwd(h, plan.ptr(), bufs, n, *ptrs, _stream()))
     return o, lse, plan
 
 
-def _bwd_core(q, k, v, o, lse, do, mask, score, scale, block_mask, tiles, plan=None):
-    """Backward through fa_bwd -> (dq, dk, dv).  ``plan`` is the forward's
-    plan when the caller has it (same problem), else one is looked up."""
+def _bwd_core(q, k, v, o, lse, do, mask, score, scale, block_mask, tiles, mods=None, plan=None):
+    """Backward through fa_bwd (fa_mods_bwd with user mods) -> (dq, dk, dv).
+    ``plan`` is the forward's plan when the caller has it (same problem),
+    else one is looked up."""
     torch = _torch()
     _check_inputs(q, k, v)
     if do.dtype != q.dtype:
@@ -240,8 +372,9 @@ def _bwd_core(q, k, v, o, lse, do, mask, score, scale, block_mask, tiles, plan=N
     if o.shape != q.shape or do.shape != q.shape or lse.shape != q.shape[:3]:
         raise ValueError("o / do / lse shapes do not match q")
     if plan is None:
-        if block_mask is None and mask is not None and not mask.is_trivial:
-            block_mask = _internal_block_mask(mask, q.shape[0], q.shape[2], k.shape[2], q.device)
+        block_mask = _tables_for(mask, mods, block_mask, q, k)
+        if mods is not None:
+            tiles = _MODS_TILES[_dtype_code(q)[1]]
         plan = _get_plan(q, k, mask, score, scale, block_mask, tiles)
     lib = _lib.load()
     ws_bytes = lib.fa_bwd_workspace_bytes(plan.ptr())
@@ -249,10 +382,18 @@ def _bwd_core(q, k, v, o, lse, do, mask, score, scale, block_mask, tiles, plan=N
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
-    _lib.check(lib.fa_bwd(plan.ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
-                          do.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(),
-                          ws.numel(), _stream()))
+    ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), do.data_ptr(), dq.data_ptr(),
+            dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws.numel())
+    if mods is None:
+        _lib.check(lib.fa_bwd(plan.ptr(), *ptrs, _stream()))
+    else:
+        h, bufs, n = _mods_args(mods, plan, q, score)
+        _lib.check(lib.fa_mods_bwd(h, plan.ptr(), bufs, n, *ptrs, _stream()))
     return dq, dk, dv
+
+
+# tiles of the run-time compiled kernels (fixed at compile time)
+_MODS_TILES = {"bf16": (128, 64), "fp32": (128, 32)}
 
 
 def _sparse(mask) -> bool:
@@ -272,11 +413,12 @@ def _as4d(t):
 
 
 def _stage_plan(q4, k4, mask_mod, block_r, block_c, scale=None):
-    mask = _as_mask_spec(mask_mod)
-    bm = None
-    if mask is not None and not mask.is_trivial:
-        bm = _internal_block_mask(mask, q4.shape[0], q4.shape[2], k4.shape[2], q4.device)
-    return _get_plan(q4, k4, mask, None, scale, bm, _ref_tiles(q4, block_r, block_c, bm is not None))
+    """(plan, user mods) of a reference-signature backward stage."""
+    mask, _, mods = _resolve(mask_mod, None)
+    bm = _tables_for(mask, mods, None, q4, k4)
+    tiles = _MODS_TILES[_dtype_code(q4)[1]] if mods is not None else \
+        _ref_tiles(q4, block_r, block_c, bm is not None)
+    return _get_plan(q4, k4, mask, None, scale, bm, tiles), mods
 
 
 def flash_attention_bwd_preprocess(o_flat, do_flat, block_r: int = DEFAULT_BLOCK_R,
@@ -287,7 +429,7 @@ def flash_attention_bwd_preprocess(o_flat, do_flat, block_r: int = DEFAULT_BLOCK
     _check_interpret(interpret)
     torch = _torch()
     o4, do4 = _dense16(_as4d(o_flat)), _dense16(_as4d(do_flat).to(o_flat.dtype))
-    plan = _stage_plan(o4, o4, None, block_r, DEFAULT_BLOCK_C)
+    plan, _ = _stage_plan(o4, o4, None, block_r, DEFAULT_BLOCK_C)
     delta = torch.empty(o4.shape[:3], device=o4.device, dtype=torch.float32)
     _lib.check(_lib.load().fa_bwd_preprocess(plan.ptr(), o4.data_ptr(), do4.data_ptr(), delta.data_ptr(),
                                              _stream()))
@@ -315,10 +457,15 @@ def flash_attention_bwd_dkv(q_flat, k_flat, v_flat, do_flat, logsumexp_flat, d_f
     torch = _torch()
     q4, k4, v4, do4, lse, delta = _stage_inputs(q_flat, k_flat, v_flat, do_flat, logsumexp_flat, d_flat,
                                                 qk_scale, softmax_scale)
-    plan = _stage_plan(q4, k4, mask_mod, block_r, block_c, qk_scale)
+    plan, mods = _stage_plan(q4, k4, mask_mod, block_r, block_c, qk_scale)
     dk, dv = torch.empty_like(k4), torch.empty_like(v4)
-    _lib.check(_lib.load().fa_bwd_dkdv(plan.ptr(), q4.data_ptr(), k4.data_ptr(), v4.data_ptr(), do4.data_ptr(),
-                                       lse.data_ptr(), delta.data_ptr(), dk.data_ptr(), dv.data_ptr(), _stream()))
+    ptrs = (q4.data_ptr(), k4.data_ptr(), v4.data_ptr(), do4.data_ptr(), lse.data_ptr(), delta.data_ptr(),
+            dk.data_ptr(), dv.data_ptr())
+    if mods is None:
+        _lib.check(_lib.load().fa_bwd_dkdv(plan.ptr(), *ptrs, _stream()))
+    else:
+        h, bufs, n = _mods_args(mods, plan, q4, None)
+        _lib.check(_lib.load().fa_mods_bwd_dkdv(h, plan.ptr(), bufs, n, *ptrs, _stream()))
     return dk.reshape(k_flat.shape), dv.reshape(v_flat.shape)
 
 
@@ -331,10 +478,15 @@ def flash_attention_bwd_dq(q_flat, k_flat, v_flat, do_flat, logsumexp_flat, d_fl
     torch = _torch()
     q4, k4, v4, do4, lse, delta = _stage_inputs(q_flat, k_flat, v_flat, do_flat, logsumexp_flat, d_flat,
                                                 qk_scale, softmax_scale)
-    plan = _stage_plan(q4, k4, mask_mod, block_r, block_c, qk_scale)
+    plan, mods = _stage_plan(q4, k4, mask_mod, block_r, block_c, qk_scale)
     dq = torch.empty_like(q4)
-    _lib.check(_lib.load().fa_bwd_dq(plan.ptr(), q4.data_ptr(), k4.data_ptr(), v4.data_ptr(), do4.data_ptr(),
-                                     lse.data_ptr(), delta.data_ptr(), dq.data_ptr(), _stream()))
+    ptrs = (q4.data_ptr(), k4.data_ptr(), v4.data_ptr(), do4.data_ptr(), lse.data_ptr(), delta.data_ptr(),
+            dq.data_ptr())
+    if mods is None:
+        _lib.check(_lib.load().fa_bwd_dq(plan.ptr(), *ptrs, _stream()))
+    else:
+        h, bufs, n = _mods_args(mods, plan, q4, None)
+        _lib.check(_lib.load().fa_mods_bwd_dq(h, plan.ptr(), bufs, n, *ptrs, _stream()))
     return dq.reshape(q_flat.shape)
 
 
@@ -348,12 +500,15 @@ class Runner:
         _check_inputs(q, k, v)
         self.q, self.k, self.v = _dense16(q), _dense16(k), _dense16(v)
         self.do = _dense16(do)
-        mask = _as_mask_spec(mask_mod if block_mask is None else block_mask.mask_mod)
+        mask, score, mods = _resolve(mask_mod if block_mask is None else block_mask.mask_mod, score_mod)
+        if mods is not None:
+            raise NotImplementedError("Runner takes the built-in mask / score descriptors; use flex_attention for "
+                                      "user callables")
         if block_mask is None and mask is not None and not mask.is_trivial:
             block_mask = _internal_block_mask(mask, q.shape[0], q.shape[2], k.shape[2], q.device)
         _, dname = _dtype_code(q)
         tiles = tiles or (128, 64 if dname == "bf16" else 32)
-        self.plan = _Plan(self.q, self.k, mask, _as_score_spec(score_mod), scale, block_mask, tiles)
+        self.plan = _Plan(self.q, self.k, mask, score, scale, block_mask, tiles)
         self.block_mask = block_mask
         self.o = torch.empty_like(self.q)
         self.lse = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
@@ -414,8 +569,8 @@ def flash_attention_fwd(q, k, v, mask_mod: Optional[MaskMod] = None, block_r: in
                         num_stages: int = DEFAULT_NUM_STAGES, interpret: bool = False):
     """Forward pass -> (o, logsumexp) with logsumexp in q's dtype (``flash_attn.py:111-165``)."""
     _check_interpret(interpret)
-    mask = _as_mask_spec(mask_mod)
-    o, lse, _ = _fwd_core(q, k, v, mask, None, None, None, _ref_tiles(q, block_r, block_c, _sparse(mask)))
+    mask, _, mods = _resolve(mask_mod, None)
+    o, lse, _ = _fwd_core(q, k, v, mask, None, None, None, _ref_tiles(q, block_r, block_c, _sparse(mask)), mods)
     return o, lse.to(q.dtype)
 
 
@@ -426,9 +581,9 @@ def flash_attention_bwd(q, k, v, o, logsumexp, do, mask_mod: Optional[MaskMod] =
     """Backward pass -> (dq, dk, dv) (``flash_attn.py:410-461``).  ``logsumexp``
     may be in q's dtype (as returned by :func:`flash_attention_fwd`) or fp32."""
     _check_interpret(interpret)
-    mask = _as_mask_spec(mask_mod)
+    mask, _, mods = _resolve(mask_mod, None)
     return _bwd_core(q, k, v, o, logsumexp, do, mask, None, None, None,
-                     _ref_tiles(q, block_r, block_c, _sparse(mask)))
+                     _ref_tiles(q, block_r, block_c, _sparse(mask)), mods)
 
 
 class _FlexFn:
@@ -444,7 +599,7 @@ class _FlexFn:
             class FlexAttnFunction(torch.autograd.Function):
                 @staticmethod
                 def forward(ctx, q, k, v, cfg):
-                    o, lse, plan = _fwd_core(q, k, v, *cfg)
+                    o, lse, plan = _fwd_core(q, k, v, *cfg)  # cfg: mask, score, scale, block mask, tiles, mods
                     ctx.save_for_backward(q, k, v, o, lse)
                     ctx.cfg = cfg
                     ctx.plan = plan
@@ -466,8 +621,8 @@ def flash_attention(q, k, v, mask_mod: Optional[MaskMod] = None, block_r: int = 
                     num_stages: int = DEFAULT_NUM_STAGES, interpret: bool = False):
     """Flash attention with a custom backward (``flash_attn.py:464-504``)."""
     _check_interpret(interpret)
-    mask = _as_mask_spec(mask_mod)
-    cfg = (mask, None, None, None, _ref_tiles(q, block_r, block_c, _sparse(mask)))
+    mask, _, mods = _resolve(mask_mod, None)
+    cfg = (mask, None, None, None, _ref_tiles(q, block_r, block_c, _sparse(mask)), mods)
     o, _ = _FlexFn.get().apply(q, k, v, cfg)
     return o
 
@@ -484,15 +639,19 @@ def flex_decode(query, key, value, score_mod: Optional[ScoreSpec] = None, block_
     torch = _torch()
     if query.shape[1] != key.shape[1] and not enable_gqa:
         raise ValueError("query and key head counts differ: pass enable_gqa=True for grouped-query attention")
-    mask = None
+    mask_mod = None
     if block_mask is not None:
-        mask = _as_mask_spec(block_mask.mask_mod) if block_mask.mask_mod is not None else None
+        mask_mod = block_mask.mask_mod
         if not block_mask.has_tables:
             raise ValueError("block_mask has no kernel tables (build it with create_block_mask)")
+    mask, score, mods = _resolve(mask_mod, score_mod)
+    if mods is not None:  # user mods: the run-time compiled forward, unsplit
+        o, lse, _ = _fwd_core(query, key, value, mask, score, scale, block_mask, None, mods)
+        return (o, lse) if return_lse else o
     q, k, v = _dense16(query), _dense16(key), _dense16(value)
     _check_inputs(q, k, v)
     _, dname = _dtype_code(q)
-    plan = _get_plan(q, k, mask, _as_score_spec(score_mod), scale, block_mask, (128, 64 if dname == "bf16" else 32))
+    plan = _get_plan(q, k, mask, score, scale, block_mask, (128, 64 if dname == "bf16" else 32))
     o = torch.empty_like(q)
     lse = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
     lib = _lib.load()
@@ -514,14 +673,18 @@ def flex_attention(query, key, value, score_mod: Optional[ScoreSpec] = None,
     table entry or the defaults (bf16: 128 x 64, fp32: 128 x 32) are used."""
     if query.shape[1] != key.shape[1] and not enable_gqa:
         raise ValueError("query and key head counts differ: pass enable_gqa=True for grouped-query attention")
-    mask = None
+    mask_mod = None
     if block_mask is not None:
-        mask = _as_mask_spec(block_mask.mask_mod) if block_mask.mask_mod is not None else None
+        mask_mod = block_mask.mask_mod
         if not block_mask.has_tables:
             raise ValueError("block_mask has no kernel tables (build it with create_block_mask)")
-        if block_mask.block_size % TABLE_BLOCK and mask is not None:
-            # the dK/dV kernel walks 128-key tiles: re-derive the exact tables at 128
+    mask, score, mods = _resolve(mask_mod, score_mod)
+    if block_mask is not None and block_mask.block_size % TABLE_BLOCK:
+        # the dK/dV kernel walks 128-key tiles: re-derive the exact tables at 128
+        if mask is not None:
             block_mask = _internal_block_mask(mask, query.shape[0], query.shape[2], key.shape[2], query.device)
+        elif mods is not None and mods.mask is not None:
+            block_mask = _user_block_mask(mods.mask, query.shape[0], query.shape[1], query.shape[2], key.shape[2])
     _, dname = _dtype_code(query)
     opts = kernel_options or {}
     tiles = None
@@ -530,6 +693,6 @@ def flex_attention(query, key, value, score_mod: Optional[ScoreSpec] = None,
     else:
         tiles = tuned_tiles(query.shape[2], query.shape[3], dname, block_mask is not None) or \
             (128, 64 if dname == "bf16" else 32)
-    cfg = (mask, _as_score_spec(score_mod), scale, block_mask, tiles)
+    cfg = (mask, score, scale, block_mask, tiles, mods)
     o, lse = _FlexFn.get().apply(query, key, value, cfg)
     return (o, lse) if return_lse else o

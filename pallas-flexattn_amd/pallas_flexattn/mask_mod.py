@@ -20,6 +20,10 @@ def _is_torch(x):
     return type(x).__module__.startswith("torch")
 
 
+def _is_sym(x):
+    return type(x).__name__ == "Sym" and type(x).__module__.endswith("lowering")
+
+
 def _ones_like_bool(delta):
     if _is_torch(delta):
         import torch
@@ -47,6 +51,7 @@ class MaskSpec:
         self.name = name or self._default_name()
         self._torch_docs = {}
         self._device_docs = {}
+        self._cpu_docs = None
 
     def _default_name(self):
         parts = []
@@ -143,6 +148,8 @@ class MaskSpec:
             b, _h, q_idx, kv_idx = args
         else:
             raise TypeError("mask mod takes (q_idx, kv_idx) or (b, h, q_idx, kv_idx)")
+        if _is_sym(q_idx) or _is_sym(kv_idx):
+            return self._traced(b, q_idx, kv_idx)
         delta = q_idx - kv_idx
         m = _ones_like_bool(delta)
         if self.left >= 0:
@@ -152,6 +159,27 @@ class MaskSpec:
         if self.doc_ids is not None:
             m = m & self._same_doc(b, q_idx, kv_idx)
         return m
+
+    def _traced(self, b, q_idx, kv_idx):
+        """The mask as an expression of traced indices (when this descriptor is
+        part of a callable lowered onto the kernels, e.g. and_masks(mask, fn))."""
+        import torch
+        delta = q_idx - kv_idx
+        m = None
+        if self.left >= 0:
+            m = delta <= self.left
+        if self.right >= 0:
+            t = (-delta) <= self.right
+            m = t if m is None else (m & t)
+        if self.doc_ids is not None:
+            if self._cpu_docs is None:
+                self._cpu_docs = torch.from_numpy(self.doc_ids)
+            row = 0 if b is None else b
+            if b is None and self.doc_ids.shape[0] != 1:
+                raise ValueError("a batch-dependent document mask needs (b, h, q_idx, kv_idx) arguments")
+            t = self._cpu_docs[row, q_idx] == self._cpu_docs[row, kv_idx]
+            m = t if m is None else (m & t)
+        return True if m is None else m
 
     def _same_doc(self, b, q_idx, kv_idx):
         docs = self.doc_ids

@@ -75,6 +75,15 @@ class ScoreSpec:
 
     def __call__(self, score, b, h, q_idx, kv_idx):
         s = score
+        if type(s).__name__ == "Sym":  # traced as part of a callable lowered onto the kernels
+            import torch
+            if self.alibi is not None:
+                if "cpu" not in self._torch_slopes:
+                    self._torch_slopes["cpu"] = torch.from_numpy(self.alibi)
+                s = s + self._torch_slopes["cpu"][h] * (kv_idx - q_idx)
+            if self.softcap > 0:
+                s = self.softcap * torch.tanh(s / self.softcap)
+            return s
         if self.alibi is not None:
             if _is_torch(s):
                 import torch

@@ -62,11 +62,13 @@ def assert_close(name, got, want, tol):
                              f"worst at {i}: got {got[i]!r} want {want[i]!r} (max abs err {err.max():.3g})")
 
 
-def oracle_fwd_bwd(q, k, v, do, mask, scale=None, alibi=None, softcap=None, bwd=True):
-    o, lse = attention.forward(q, k, v, mask=mask, scale=scale, alibi_slopes=alibi, softcap=softcap)
+def oracle_fwd_bwd(q, k, v, do, mask, scale=None, alibi=None, softcap=None, bwd=True, score_fn=None):
+    o, lse = attention.forward(q, k, v, mask=mask, scale=scale, alibi_slopes=alibi, softcap=softcap,
+                               score_fn=score_fn)
     if not bwd:
         return o, lse, None
-    return o, lse, attention.backward(q, k, v, do, mask=mask, scale=scale, alibi_slopes=alibi, softcap=softcap)
+    return o, lse, attention.backward(q, k, v, do, mask=mask, scale=scale, alibi_slopes=alibi, softcap=softcap,
+                                      score_fn=score_fn)
 
 
 def assert_as_accurate(name, got, alg, exact, max_ratio=1.5, rms_ratio=1.25):

@@ -145,6 +145,7 @@ def test_scan_finds_planted_copy():
 def test_no_early_reads_of_asm_mfma_results(tmp_path):
     sys.path.insert(0, os.path.join(ROOT, "pallas-flexattn_amd"))
     import build as b
+    b.write_rtc_sources()
     flags = [f for f in b.FLAGS if f not in ("-shared", "-fPIC")]
     out = tmp_path / "capi.s"
     res = subprocess.run([b.HIPCC, *flags, "--cuda-device-only", "-S", *b.SOURCES, "-o", str(out)],
@@ -159,6 +160,38 @@ def test_no_early_reads_of_asm_mfma_results(tmp_path):
     assert not m0, "inline asm leaves M0 changed: " + "; ".join(m0[:10])
     late = late_operands(text)
     assert not late, "\n".join(f"{k} line {ln}: {ws} wait states: {ins}" for k, ln, ws, ins in late[:20])
+
+
+@pytest.mark.skipif(shutil.which("hipcc") is None and not os.path.exists("/opt/rocm/bin/hipcc"),
+                    reason="hipcc not available")
+def test_user_mod_kernels_pass_the_same_scans(tmp_path):
+    """The kernels compiled at run time for user mods are the same templates with a
+    generated policy (user mask on partial tiles, user score with its derivative, tensor
+    reads); compiled here with the library's compiler and flags, as the run-time compile
+    does, they must pass the same scans."""
+    import torch
+    sys.path.insert(0, os.path.join(ROOT, "pallas-flexattn_amd"))
+    import build as b
+    from pallas_flexattn import lowering as L
+    bias = torch.randn(4, 64)
+    mods = L.UserMods(L.lower_mask(lambda q, kv: (kv < 64) | ((q >= kv) & ((q - kv) % 3 != 1))),
+                      L.lower_score(lambda s, bb, h, q, kv: 20.0 * torch.tanh((s + bias[h, kv % 64]) / 20.0)))
+    src = tmp_path / "user_mods.hip"
+    inst = "\n".join(f"template __global__ void fa::{k}<128, 64, 4, true, UserMod>(fa::{a});"
+                     for k, a in (("fwd_bf16_kernel", "FwdArgs"), ("dq_bf16_kernel", "BwdArgs"),
+                                  ("dkdv_bf16_kernel", "BwdArgs")))
+    csrc = os.path.join(ROOT, "pallas-flexattn_amd", "csrc")
+    src.write_text(f'#include "fwd_bf16.h"\n#include "bwd_bf16.h"\n{mods.source}\n{inst}\n')
+    flags = [f for f in b.FLAGS if f not in ("-shared", "-fPIC")]
+    out = tmp_path / "user_mods.s"
+    res = subprocess.run([b.HIPCC, *flags, "-I" + csrc, "--cuda-device-only", "-S", str(src), "-o", str(out)],
+                         capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr[-2000:]
+    text = out.read_text()
+    assert text.count("v_mfma") > 100
+    for name, found in (("early", early_touches(text)), ("late", late_operands(text))):
+        assert not found, name + "\n" + "\n".join(f"{k} line {ln}: {ws}: {ins}" for k, ln, ws, ins in found[:20])
+    assert not m0_unrestored(text)
 
 
 def m0_unrestored(asm_text):

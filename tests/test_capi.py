@@ -13,7 +13,7 @@ HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))
 
 def declared_functions():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char \*)\s*(fa_\w+)\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|void|const char \*)\s*(fa_\w+)\(", text, re.M)))
 
 
 def test_library_exports_every_declared_symbol():

@@ -80,15 +80,18 @@ def test_score_spec_matches_formula():
         pf.compose_score_mods(pf.softcap_score_mod(5.0), pf.alibi_score_mod(4))
 
 
-def test_interpret_mode_and_unsupported_callables_raise():
+def test_interpret_mode_and_untraceable_callables_raise():
     torch = pytest.importorskip("torch")
     x = torch.zeros(1, 1, 8, 32)
     with pytest.raises(NotImplementedError):
         pf.flash_attention(x, x, x, interpret=True)
-    from pallas_flexattn.flash_attn import _as_mask_spec, _as_score_spec
-    with pytest.raises(NotImplementedError):
-        _as_mask_spec(lambda q, k: q >= k)
-    with pytest.raises(NotImplementedError):
-        _as_score_spec(lambda s, b, h, q, k: s)
+    from pallas_flexattn.flash_attn import _resolve
+    # callables are traced and lowered; Python control flow on traced indices cannot be
+    with pytest.raises(NotImplementedError, match="control flow"):
+        _resolve(lambda q, k: (q >= k) if q > 0 else (q < k), None)
+    with pytest.raises(NotImplementedError, match="cannot be lowered"):
+        _resolve(None, lambda s, b, h, q, k: torch.erf(s))
+    mask, score, mods = _resolve(lambda q, k: q >= k, lambda s, b, h, q, k: s * 2.0)
+    assert mask is None and score is None and mods.mask is not None and mods.score is not None
     with pytest.raises(ValueError):  # host tensors are rejected, never computed on the CPU
         pf.flash_attention_fwd(x, x, x)

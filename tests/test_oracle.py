@@ -92,6 +92,23 @@ def test_gqa_equals_repeated_kv():
     np.testing.assert_allclose(dv, dv2.reshape(2, 2, 3, 12, 8).sum(2), atol=1e-12)
 
 
+def test_score_fn_reduces_to_alibi_and_softcap():
+    """score_fn with the ALiBi + soft-cap formula gives the built-in mods' results exactly."""
+    q, k, v, do = (_rand((1, 2, 9, 4), s) for s in range(4))
+    slopes = np.array([1.0, 0.25])
+
+    def fn(s, b, h, qi, ki):
+        t = np.tanh((s + slopes[h] * (ki - qi)) / 5.0)
+        return 5.0 * t, 1.0 - t * t
+    a = attention.forward(q, k, v, alibi_slopes=slopes, softcap=5.0)
+    c = attention.forward(q, k, v, score_fn=fn)
+    np.testing.assert_allclose(a[0], c[0], atol=1e-13)
+    ga = attention.backward(q, k, v, do, alibi_slopes=slopes, softcap=5.0)
+    gc = attention.backward(q, k, v, do, score_fn=fn)
+    for x, y in zip(ga, gc):
+        np.testing.assert_allclose(x, y, atol=1e-13)
+
+
 def test_score_mods_match_direct_formula():
     q, k, v = (_rand((1, 2, 9, 4), s) for s in range(3))
     slopes = np.array([1.0, 0.25])
@@ -106,7 +123,17 @@ def test_score_mods_match_direct_formula():
 
 
 # ----------------------------------------------------------- backward -----
-@pytest.mark.parametrize("mods", [dict(), dict(alibi_slopes=np.array([0.5, 0.125, 1.0, 2.0]), softcap=3.0)])
+def _capped_bias(s, b, h, q, kv):
+    t = np.tanh(s / 3.0)
+    return 3.0 * t + 0.05 * h * (kv - q), 1.0 - t * t
+
+
+def _quadratic(s, b, h, q, kv):
+    return 0.1 * s * s + s + 0.01 * (q % 3), 0.2 * s + 1.0
+
+
+@pytest.mark.parametrize("mods", [dict(), dict(alibi_slopes=np.array([0.5, 0.125, 1.0, 2.0]), softcap=3.0),
+                                  dict(score_fn=_capped_bias), dict(score_fn=_quadratic)])
 def test_backward_matches_finite_differences(mods):
     B, Hq, Hkv, S, D = 1, 4, 2, 7, 5
     q, do = _rand((B, Hq, S, D), 0), _rand((B, Hq, S, D), 3)
