@@ -154,8 +154,10 @@ def cpu_baseline(cfg, arrays, pairs_per_head, target_s):
 def bench_decode(args):
     """Decoding-shaped forward: one query per (batch, q head) against a long
     KV cache, bf16, no mask (B8 Hq32 Hkv8 Skv32768 D128).  HBM-bound: the
-    metric is KV-cache bytes read per second, split-KV (flex_decode) next to
-    the unsplit forward (flex_attention)."""
+    metric is KV-cache bytes read per second by split-KV flex_decode (the
+    query heads of each GQA group packed into one tile, so K / V are read once
+    per group), next to the same cache paged (64 pages of 512 keys per row,
+    shuffled) and the unsplit forward."""
     import torch
     import pallas_flexattn as pf
     B, Hq, Hkv, Sq, Skv, D = 8, 32, 8, 1, 32768, 128
@@ -163,15 +165,29 @@ def bench_decode(args):
     q = torch.randn(B, Hq, Sq, D, device="cuda", generator=g).to(torch.bfloat16)
     k = torch.randn(B, Hkv, Skv, D, device="cuda", generator=g).to(torch.bfloat16)
     v = torch.randn(B, Hkv, Skv, D, device="cuda", generator=g).to(torch.bfloat16)
+    ps = 512
+    npg = Skv // ps
+    perm = torch.randperm(B * npg, generator=torch.Generator().manual_seed(7)).view(B, npg).to(torch.int32)
+    kc = k.view(B, Hkv, npg, ps, D).permute(0, 2, 1, 3, 4).reshape(B * npg, Hkv, ps, D)[perm.view(-1).argsort()]
+    vc = v.view(B, Hkv, npg, ps, D).permute(0, 2, 1, 3, 4).reshape(B * npg, Hkv, ps, D)[perm.view(-1).argsort()]
+    kc, vc = kc.contiguous(), vc.contiguous()
+    pt = perm.cuda()
     stream = torch.cuda.current_stream()
-    split = lambda: pf.flex_decode(q, k, v, enable_gqa=True)
-    plain = lambda: pf.flex_attention(q, k, v, enable_gqa=True)
+    split = lambda: pf.flex_decode(q, k, v, enable_gqa=True)  # noqa: E731
+    paged = lambda: pf.flex_decode(q, kc, vc, enable_gqa=True, page_table=pt)  # noqa: E731
+    plain = lambda: pf.flex_attention(q, k, v, enable_gqa=True)  # noqa: E731
+    o_s, o_p = split(), paged()
+    torch.cuda.synchronize()
+    if not torch.equal(o_s, o_p):
+        raise SystemExit("paged and contiguous decode differ")
     t0 = time.perf_counter()
     while time.perf_counter() - t0 < 0.5:
         split()
+        paged()
         plain()
         torch.cuda.synchronize()
     ms_split = time_region(split, args.steps, stream)
+    ms_paged = time_region(paged, args.steps, stream)
     ms_plain = time_region(plain, args.steps, stream)
     kv_bytes = 2.0 * B * Hkv * Skv * D * 2
     gbs = kv_bytes / (ms_split * 1e-3) / 1e9
@@ -181,9 +197,11 @@ def bench_decode(args):
         "dtype": "bf16", "data": "synthetic (torch normals rounded to bf16)",
         "config": {"workload": "decode B8 Hq32 Hkv8 Sq1 Skv32768 D128 bf16, no mask", "B": B, "Hq": Hq, "Hkv": Hkv,
                    "Sq": Sq, "Skv": Skv, "D": D},
+        "paged_ms": round(ms_paged, 4), "paged_gbs": round(kv_bytes / (ms_paged * 1e-3) / 1e9, 1),
+        "page_size": ps,
         "unsplit_forward_ms": round(ms_plain, 4),
-        "roofline": {"kernel": "fwd (split-KV) + merge", "bound": "hbm", "achieved": round(gbs, 1), "peak": 8000.0,
-                     "unit": "GB/s", "frac": round(gbs / 8000.0, 4), "traffic": None},
+        "roofline": {"kernel": "fwd (split-KV, GQA-packed) + merge", "bound": "hbm", "achieved": round(gbs, 1),
+                     "peak": 8000.0, "unit": "GB/s", "frac": round(gbs / 8000.0, 4), "traffic": None},
     }
     print(json.dumps(out), flush=True)
 

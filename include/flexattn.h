@@ -119,6 +119,26 @@ size_t fa_fwd_splitkv_workspace_bytes(const fa_params *p, int n_splits);
 int fa_fwd_splitkv(const fa_params *p, const void *q, const void *k, const void *v, void *o, float *lse,
                    int n_splits, void *workspace, size_t workspace_bytes, void *stream);
 
+/* Split-KV forward over a KV cache (decode): keys of batch row b are
+ * [0, kv_lens[b]) (kv_lens NULL: all Skv), and with a page table K / V are
+ * paged caches of shape (num_pages, Hkv, page_size, D): key t of batch row b
+ * lives in page page_table[b * max_pages + t / page_size] at row t % page_size
+ * (page_size a multiple of 64; page ids outside [0, num_pages) read as zero
+ * keys).  Without a page table K / V are the usual (B, Hkv, Skv, D).  Skv is
+ * the longest row's key count; block tables, windows and documents index the
+ * logical key positions.  bf16, window / contiguous-document masks.  Same
+ * workspace as fa_fwd_splitkv.  No reference counterpart (the reference's
+ * roadmap lists a decode kernel, CLAUDE.md:118). */
+typedef struct fa_kv_cache {
+  const int32_t *page_table; /* (B, max_pages) or NULL */
+  int32_t page_size, max_pages, num_pages;
+  const int32_t *kv_lens; /* (B) or NULL */
+} fa_kv_cache;
+size_t fa_fwd_kvcache_workspace_bytes(const fa_params *p, const fa_kv_cache *kv, int n_splits);
+int fa_fwd_kvcache(const fa_params *p, const fa_kv_cache *kv, const void *q, const void *k_cache,
+                   const void *v_cache, void *o, float *lse, int n_splits, void *workspace, size_t workspace_bytes,
+                   void *stream);
+
 /* Bytes of device scratch fa_bwd needs for these params. */
 size_t fa_bwd_workspace_bytes(const fa_params *p);
 

@@ -153,9 +153,15 @@ bool aligned16(std::initializer_list<const void*> ptrs) {
 bool interval_masks(const Problem& p) { return p.q_doc == nullptr || p.doc_start != nullptr; }
 
 // ------------------------------------------------------------- forward ----
+// Work items of the forward: (batch, q head, query tile), or with GQA row
+// packing (batch, kv head, tile of the group's g * Sq rows).
+int fwd_items(const Problem& p, int pack, int bm) {
+  return pack > 1 ? p.B * p.Hkv * cdiv(pack * p.Sq, bm) : p.B * p.Hq * cdiv(p.Sq, bm);
+}
+
 template <typename T, int D, int BN, int NW, bool M>
 int run_fwd(const FwdArgs& a, hipStream_t s) {
-  const int grid = a.p.B * a.p.Hq * cdiv(a.p.Sq, 32 * NW);
+  const int grid = fwd_items(a.p, a.pack, 32 * NW);
   if constexpr (sizeof(T) == 2) {
     if (interval_masks(a.p)) {  // bf16: LDS-DMA + transposing-read kernel
       hipLaunchKernelGGL((fa::fwd_bf16_kernel<D, BN, NW, M>), dim3(grid * a.n_splits), dim3(NW * 64), 0, s, a);
@@ -166,9 +172,10 @@ int run_fwd(const FwdArgs& a, hipStream_t s) {
       return launch_status();
     }
   }
-  FwdArgs g = a;  // the generic kernel has no split-KV form
+  FwdArgs g = a;  // the generic kernel has no split-KV, packed or paged form
   g.n_splits = 1;
-  hipLaunchKernelGGL((fa::fwd_kernel<T, D, BN, NW, M>), dim3(grid), dim3(NW * 64), 0, s, g);
+  g.pack = 0;
+  hipLaunchKernelGGL((fa::fwd_kernel<T, D, BN, NW, M>), dim3(fwd_items(a.p, 0, 32 * NW)), dim3(NW * 64), 0, s, g);
   return launch_status();
 }
 
@@ -333,11 +340,23 @@ int device_cus() {
   return cached[dev];
 }
 
+// GQA row packing: for query blocks shorter than a tile, the g = Hq / Hkv
+// heads sharing a kv head run as one work item, so each K / V tile is read
+// once for the group instead of once per head (decode shapes).  Needs the
+// bf16 interval kernel and block tables (if any) shared by all heads with Sq
+// inside one mask block.
+int choose_pack(const fa_params* p, const Tiles& t, const Problem& pr) {
+  const int g = p->Hq / p->Hkv;
+  if (p->dtype != FA_DTYPE_BF16 || !interval_masks(pr) || g < 2 || p->Sq >= t.bm) return 0;
+  if (pr.has_tables && (pr.tab_h != 1 || p->Sq > pr.mblk_q)) return 0;
+  return g;
+}
+
 // Split-KV: the requested count (<= 0: about two workgroups per CU, at least
 // four key tiles per split), or 1 where the generic kernel runs.
 int choose_splits(const fa_params* p, const Tiles& t, const Problem& pr, int requested) {
   if (p->dtype != FA_DTYPE_BF16 || !interval_masks(pr)) return 1;
-  const int items = p->B * p->Hq * cdiv(p->Sq, t.bm);
+  const int items = fwd_items(pr, choose_pack(p, t, pr), t.bm);
   const int max_by_keys = cdiv(p->Skv, 4 * t.bn);
   int n = requested;
   if (n <= 0) n = cdiv(2 * device_cus(), items);
@@ -348,6 +367,53 @@ int choose_splits(const fa_params* p, const Tiles& t, const Problem& pr, int req
 
 size_t split_bytes(const fa_params* p, int n) {
   return n > 1 ? (size_t)n * p->B * p->Hq * p->Sq * (p->D + 2) * sizeof(float) : 0;
+}
+
+// The forward entry points: fa_fwd (split = false), fa_fwd_splitkv and
+// fa_fwd_kvcache (split-KV, optional paged / per-batch-length keys).
+int fwd_launch(const fa_params* p, const fa_kv_cache* kv, const void* q, const void* k, const void* v, void* o,
+               float* lse, bool split, int n_splits, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!p) return FA_ERR_NULL;
+  if (n_splits > 64) return FA_ERR_SHAPE;
+  Tiles t;
+  int rc = default_tiles(p, &t);
+  if (rc) return rc;
+  FwdArgs a;
+  rc = build_problem(p, t, &a.p);
+  if (rc) return rc;
+  if (!q || !k || !v || !o || !lse) return FA_ERR_NULL;
+  if (!aligned16({q, k, v, o})) return FA_ERR_SHAPE;
+  if (a.p.has_tables && (a.p.mblk_q % t.bm || a.p.mblk_kv % t.bn)) return FA_ERR_TABLES;
+  if (a.p.has_tables && !a.p.kv_num && !a.p.full_kv_num) return FA_ERR_TABLES;
+  if (kv) {  // paged / per-batch-length keys: the bf16 interval kernel only
+    if (p->dtype != FA_DTYPE_BF16 || !interval_masks(a.p)) return FA_ERR_UNSUPPORTED;
+    if (kv->page_table) {
+      if (kv->page_size < t.bn || kv->page_size % t.bn || kv->num_pages < 1) return FA_ERR_SHAPE;
+      if ((long long)kv->max_pages * kv->page_size < p->Skv) return FA_ERR_SHAPE;
+      a.page_table = kv->page_table;
+      a.page_size = kv->page_size;
+      a.max_pages = kv->max_pages;
+      a.num_pages = kv->num_pages;
+    }
+    a.kv_lens = kv->kv_lens;
+  }
+  a.pack = choose_pack(p, t, a.p);
+  a.n_splits = split ? choose_splits(p, t, a.p, n_splits) : 1;
+  if (a.n_splits > 1) {
+    if (!workspace || workspace_bytes < split_bytes(p, a.n_splits) || !aligned16({workspace}))
+      return FA_ERR_WORKSPACE;
+    a.part = static_cast<float*>(workspace);
+  }
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.lse = lse;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool m = has_mods(a.p);
+  if (p->dtype == FA_DTYPE_BF16)
+    return m ? fwd_d<uint16_t, 64, true>(a, p->D, t.bm, s) : fwd_d<uint16_t, 64, false>(a, p->D, t.bm, s);
+  return m ? fwd_d<float, 32, true>(a, p->D, t.bm, s) : fwd_d<float, 32, false>(a, p->D, t.bm, s);
 }
 
 #include "user_mods.h"
@@ -385,59 +451,24 @@ size_t fa_fwd_splitkv_workspace_bytes(const fa_params* p, int n_splits) {
 
 int fa_fwd_splitkv(const fa_params* p, const void* q, const void* k, const void* v, void* o, float* lse,
                    int n_splits, void* workspace, size_t workspace_bytes, void* stream) {
-  if (!p) return FA_ERR_NULL;
-  if (n_splits > 64) return FA_ERR_SHAPE;
-  Tiles t;
-  int rc = default_tiles(p, &t);
-  if (rc) return rc;
-  FwdArgs a;
-  rc = build_problem(p, t, &a.p);
-  if (rc) return rc;
-  if (!q || !k || !v || !o || !lse) return FA_ERR_NULL;
-  if (!aligned16({q, k, v, o})) return FA_ERR_SHAPE;
-  if (a.p.has_tables && (a.p.mblk_q % t.bm || a.p.mblk_kv % t.bn)) return FA_ERR_TABLES;
-  if (a.p.has_tables && !a.p.kv_num && !a.p.full_kv_num) return FA_ERR_TABLES;
-  a.n_splits = choose_splits(p, t, a.p, n_splits);
-  if (a.n_splits > 1) {
-    if (!workspace || workspace_bytes < split_bytes(p, a.n_splits) || !aligned16({workspace}))
-      return FA_ERR_WORKSPACE;
-    a.part = static_cast<float*>(workspace);
-  }
-  a.q = q;
-  a.k = k;
-  a.v = v;
-  a.o = o;
-  a.lse = lse;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool m = has_mods(a.p);
-  if (p->dtype == FA_DTYPE_BF16)
-    return m ? fwd_d<uint16_t, 64, true>(a, p->D, t.bm, s) : fwd_d<uint16_t, 64, false>(a, p->D, t.bm, s);
-  return m ? fwd_d<float, 32, true>(a, p->D, t.bm, s) : fwd_d<float, 32, false>(a, p->D, t.bm, s);
+  return fwd_launch(p, nullptr, q, k, v, o, lse, true, n_splits, workspace, workspace_bytes, stream);
 }
 
 int fa_fwd(const fa_params* p, const void* q, const void* k, const void* v, void* o, float* lse,
            void* stream) {
-  if (!p) return FA_ERR_NULL;
-  Tiles t;
-  int rc = default_tiles(p, &t);
-  if (rc) return rc;
-  FwdArgs a;
-  rc = build_problem(p, t, &a.p);
-  if (rc) return rc;
-  if (!q || !k || !v || !o || !lse) return FA_ERR_NULL;
-  if (!aligned16({q, k, v, o})) return FA_ERR_SHAPE;
-  if (a.p.has_tables && (a.p.mblk_q % t.bm || a.p.mblk_kv % t.bn)) return FA_ERR_TABLES;
-  if (a.p.has_tables && !a.p.kv_num && !a.p.full_kv_num) return FA_ERR_TABLES;
-  a.q = q;
-  a.k = k;
-  a.v = v;
-  a.o = o;
-  a.lse = lse;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool m = has_mods(a.p);
-  if (p->dtype == FA_DTYPE_BF16)
-    return m ? fwd_d<uint16_t, 64, true>(a, p->D, t.bm, s) : fwd_d<uint16_t, 64, false>(a, p->D, t.bm, s);
-  return m ? fwd_d<float, 32, true>(a, p->D, t.bm, s) : fwd_d<float, 32, false>(a, p->D, t.bm, s);
+  return fwd_launch(p, nullptr, q, k, v, o, lse, false, 1, nullptr, 0, stream);
+}
+
+size_t fa_fwd_kvcache_workspace_bytes(const fa_params* p, const fa_kv_cache* kv, int n_splits) {
+  (void)kv;
+  return fa_fwd_splitkv_workspace_bytes(p, n_splits);
+}
+
+int fa_fwd_kvcache(const fa_params* p, const fa_kv_cache* kv, const void* q, const void* k_cache,
+                   const void* v_cache, void* o, float* lse, int n_splits, void* workspace, size_t workspace_bytes,
+                   void* stream) {
+  if (!kv) return FA_ERR_NULL;
+  return fwd_launch(p, kv, q, k_cache, v_cache, o, lse, true, n_splits, workspace, workspace_bytes, stream);
 }
 
 size_t fa_bwd_workspace_bytes(const fa_params* p) {

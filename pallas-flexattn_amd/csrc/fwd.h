@@ -31,6 +31,18 @@ struct FwdArgs {
   // (n_splits, B*Hq*Sq, D) floats, then (n_splits, B*Hq*Sq, 2).
   int n_splits = 1;
   float* part = nullptr;
+  // bf16 DMA kernel only:
+  // GQA row packing (pack > 1): a work item is (batch, kv head, BM rows) of
+  // the g = Hq / Hkv query heads' rows taken as one sequence of g * Sq rows
+  // (row r: q head hk * g + r / Sq, query r % Sq; in memory these rows are
+  // contiguous), so a K / V tile serves the whole group.  For short Sq (decode).
+  int pack = 0;
+  // Paged K / V: k, v are (num_pages, Hkv, page_size, D) caches and key t of
+  // batch row b sits in page page_table[b * max_pages + t / page_size].
+  const int* page_table = nullptr;
+  int page_size = 0, max_pages = 0, num_pages = 0;
+  // Keys of batch row b are [0, kv_lens[b]) (each <= Skv); null: all Skv.
+  const int* kv_lens = nullptr;
 };
 
 // A tile of a walk whose table entry may still be in flight: fetch() issues

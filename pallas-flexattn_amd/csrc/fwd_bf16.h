@@ -1,6 +1,7 @@
 // bf16 forward FlexAttention kernel for gfx950 (the main forward path).
 //
-// Work item: (batch, q head, BM = 32*NW query rows); wave w owns rows
+// Work item: (batch, q head, BM = 32*NW query rows) -- or, with GQA row
+// packing, (batch, kv head, BM of the group's g * Sq rows); wave w owns rows
 // q0 + 32w .. +31 for the whole kv walk.
 //
 // Per kv tile of BN keys (double-buffered in LDS, one barrier per tile):
@@ -56,16 +57,28 @@ void fwd_bf16_kernel(FwdArgs a) {
   const Problem& P = a.p;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 31, hh = lane >> 5;
-  const int nqt = (P.Sq + BM - 1) / BM;
-  const int n_items = P.B * P.Hq * nqt;
+  // A work item's rows: Sq queries of one q head, or with GQA packing the
+  // g * Sq rows of a kv head's q heads (contiguous in memory).
+  const int g = P.Hq / P.Hkv;
+  const bool pack = a.pack > 1;
+  const int rows = pack ? g * P.Sq : P.Sq;
+  const int nheads = pack ? P.B * P.Hkv : P.B * P.Hq;
+  const int nqt = (rows + BM - 1) / BM;
+  const int n_items = nheads * nqt;
   const int split = a.n_splits > 1 ? (int)blockIdx.x / n_items : 0;
   int head, qt;
-  work_item((int)blockIdx.x - split * n_items, P.B * P.Hq, nqt, P.xcd_remap, P.head_group_q, false, &head, &qt);
-  const int b = head / P.Hq, h = head - b * P.Hq;
-  const int hk = h / (P.Hq / P.Hkv);
+  work_item((int)blockIdx.x - split * n_items, nheads, nqt, P.xcd_remap, pack ? 1 : P.head_group_q, false, &head,
+            &qt);
+  const int b = head / (pack ? P.Hkv : P.Hq);
+  const int hk = pack ? head - b * P.Hkv : (head - b * P.Hq) / g;
+  const size_t row0 = pack ? (size_t)(b * P.Hq + hk * g) * P.Sq : (size_t)head * P.Sq;  // first row in memory
   const int q0 = qt * BM;
-  const int qw = q0 + 32 * w + lr;
-  const bool qvalid = qw < P.Sq;
+  const int rw = q0 + 32 * w + lr;  // this lane's row of the work item
+  const bool qvalid = rw < rows;
+  const int qw = pack ? rw % P.Sq : rw;                           // query position
+  const int h = pack ? hk * g + rw / P.Sq : head - b * P.Hq;      // q head (per lane when packed)
+  // keys of this batch row
+  const int skv = a.kv_lens ? max(0, min(a.kv_lens[b], P.Skv)) : P.Skv;
 
   const char* kbase_ptr = static_cast<const char*>(a.k) + (size_t)(b * P.Hkv + hk) * P.Skv * RB;
   const char* vbase_ptr = static_cast<const char*>(a.v) + (size_t)(b * P.Hkv + hk) * P.Skv * RB;
@@ -73,9 +86,9 @@ void fwd_bf16_kernel(FwdArgs a) {
   // Q rows as B operands (rows past the sequence read as zero)
   frag qf[KSTEPS];
   {
-    const i32x4 rq = make_rsrc(static_cast<const char*>(a.q) + (size_t)head * P.Sq * RB, (uint32_t)P.Sq * RB);
+    const i32x4 rq = make_rsrc(static_cast<const char*>(a.q) + row0 * RB, (uint32_t)rows * RB);
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) qf[s] = buf_load16(rq, qw * RB + (2 * s + hh) * 16);
+    for (int s = 0; s < KSTEPS; ++s) qf[s] = buf_load16(rq, rw * RB + (2 * s + hh) * 16);
   }
   const float slope = P.alibi ? P.alibi[h] : 0.f;
   const float cap_inv = P.softcap > 0.f ? 1.0f / P.softcap : 0.f;
@@ -83,6 +96,7 @@ void fwd_bf16_kernel(FwdArgs a) {
   // arbitrary document labels to the generic kernel)
   int klo, khi;
   key_interval(P, b, qw, &klo, &khi);
+  khi = min(khi, skv - 1);
 
   // loop-invariant LDS / global offsets
   int dma_off_k[IPW], dma_off_v[IPW];
@@ -116,12 +130,14 @@ void fwd_bf16_kernel(FwdArgs a) {
   walk.sub = P.mblk_kv / BN;
   walk.nblk = P.n_kvblk;
   walk.dense = !P.has_tables;
-  walk.ntiles_dense = (P.Skv + BN - 1) / BN;
+  walk.ntiles_dense = (skv + BN - 1) / BN;
   walk.dense_masked = P.has_mask;
   walk.full = walk.part = nullptr;
   walk.nfull = walk.npart = 0;
   if (P.has_tables) {
-    const int row = tab_row(P, b, h, q0 / P.mblk_q, P.n_qblk);
+    // packed rows share table row 0 of their batch row (the host packs only
+    // with tables broadcast over heads and Sq within one mask block)
+    const int row = pack ? tab_row(P, b, 0, 0, P.n_qblk) : tab_row(P, b, h, q0 / P.mblk_q, P.n_qblk);
     if (P.full_kv_num) {
       walk.nfull = clamp_count(scalar_load(P.full_kv_num, row), P.kv_width);
       walk.full = P.full_kv_idx + (size_t)row * P.kv_width;
@@ -135,10 +151,21 @@ void fwd_bf16_kernel(FwdArgs a) {
 
   // HBM -> LDS copies of the tile starting at key kb into buffer `buf`
   auto issue = [&](int kb, int buf) {
-    kb = kb < P.Skv ? kb : P.Skv;
-    const uint32_t range = (uint32_t)(P.Skv - kb) * RB;
-    const i32x4 rk = make_rsrc(kbase_ptr + (size_t)kb * RB, range);
-    const i32x4 rv = make_rsrc(vbase_ptr + (size_t)kb * RB, range);
+    kb = kb < skv ? kb : skv;
+    const char* kp = kbase_ptr + (size_t)kb * RB;
+    const char* vp = vbase_ptr + (size_t)kb * RB;
+    uint32_t range = (uint32_t)(skv - kb) * RB;
+    if (a.page_table) {  // the tile lies inside one page (page_size is a multiple of BN)
+      const int pg = kb / a.page_size, off = kb - pg * a.page_size;
+      const int phys = kb < skv ? scalar_load(a.page_table + (size_t)b * a.max_pages, pg) : -1;
+      const bool ok = phys >= 0 && phys < a.num_pages;  // a bad page id reads zeros
+      const size_t at = ((size_t)(ok ? phys : 0) * P.Hkv + hk) * a.page_size + off;
+      kp = static_cast<const char*>(a.k) + at * RB;
+      vp = static_cast<const char*>(a.v) + at * RB;
+      range = ok ? (uint32_t)min(a.page_size - off, skv - kb) * RB : 0u;
+    }
+    const i32x4 rk = make_rsrc(kp, range);
+    const i32x4 rv = make_rsrc(vp, range);
     char* kl = lds + buf * TILE;
     char* vl = lds + (2 + buf) * TILE;
 #pragma unroll
@@ -250,8 +277,8 @@ void fwd_bf16_kernel(FwdArgs a) {
       issue(kb_next, buf ^ 1);
     }
     if (it + 2 < it1) ref_next = walk.fetch(it + 2);
-    if (kbase < P.Skv) {  // workgroup-uniform
-      masked = masked || (kbase + BN > P.Skv);
+    if (kbase < skv) {  // workgroup-uniform
+      masked = masked || (kbase + BN > skv);
       const char* kl = lds + buf * TILE;
       const char* vl = lds + (2 + buf) * TILE;
 
@@ -342,10 +369,10 @@ void fwd_bf16_kernel(FwdArgs a) {
   const float lt = pair_sum(l);
   const float inv = lt > 0.f ? 1.0f / lt : 0.f;
   if (a.n_splits > 1) {  // partial O (relative to 2^m) and (m, l) for the merge
-    const size_t rows = (size_t)P.B * P.Hq * P.Sq;
-    const size_t row = (size_t)head * P.Sq + qw;
+    const size_t all_rows = (size_t)P.B * P.Hq * P.Sq;
+    const size_t row = row0 + rw;
     if (qvalid) {
-      float* po = a.part + ((size_t)split * rows + row) * D;
+      float* po = a.part + ((size_t)split * all_rows + row) * D;
 #pragma unroll
       for (int i = 0; i < DT; ++i)
 #pragma unroll
@@ -353,7 +380,7 @@ void fwd_bf16_kernel(FwdArgs a) {
           *reinterpret_cast<f32x4*>(po + 32 * i + 8 * j + 4 * hh) =
               f32x4{oacc[i][4 * j], oacc[i][4 * j + 1], oacc[i][4 * j + 2], oacc[i][4 * j + 3]};
       if (hh == 0) {
-        float* pml = a.part + (size_t)a.n_splits * rows * D + ((size_t)split * rows + row) * 2;
+        float* pml = a.part + (size_t)a.n_splits * all_rows * D + ((size_t)split * all_rows + row) * 2;
         *reinterpret_cast<float2*>(pml) = make_float2(m, lt);
       }
     }
@@ -361,9 +388,9 @@ void fwd_bf16_kernel(FwdArgs a) {
   }
   // O rows of this wave, staged through the (now idle) K / V buffers
   store_rows_bf16<D>(oacc, inv, lds + w * (32 * RB),
-                     static_cast<uint16_t*>(a.o) + ((size_t)head * P.Sq + q0 + 32 * w) * D, P.Sq - (q0 + 32 * w),
+                     static_cast<uint16_t*>(a.o) + (row0 + q0 + 32 * w) * D, rows - (q0 + 32 * w),
                      lane);
-  if (qvalid && hh == 0) a.lse[(size_t)head * P.Sq + qw] = lt > 0.f ? (m + log2f(lt)) * kLn2 : -INFINITY;
+  if (qvalid && hh == 0) a.lse[row0 + rw] = lt > 0.f ? (m + log2f(lt)) * kLn2 : -INFINITY;
 }
 
 // Split-KV merge: one thread per (row, column) of O.  With the splits'

@@ -9,6 +9,8 @@ from pallas_flexattn.flash_attn import (
     mha_reference,
     flex_attention,
     flex_decode,
+    flex_attention_varlen,
+    varlen_mask,
     flash_attention_bwd_preprocess,
     flash_attention_bwd_dkv,
     flash_attention_bwd_dq,
@@ -62,6 +64,8 @@ __all__ = [
     # MI355X FlexAttention surface
     "flex_attention",
     "flex_decode",
+    "flex_attention_varlen",
+    "varlen_mask",
     "flash_attention_bwd_preprocess",
     "flash_attention_bwd_dkv",
     "flash_attention_bwd_dq",

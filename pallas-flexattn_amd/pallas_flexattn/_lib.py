@@ -58,7 +58,14 @@ class FaMaskBuild(ctypes.Structure):
     ]
 
 
-EXPORTED = ("fa_fwd", "fa_fwd_splitkv", "fa_fwd_splitkv_workspace_bytes", "fa_bwd", "fa_bwd_workspace_bytes",
+class FaKvCache(ctypes.Structure):
+    """Mirror of ``struct fa_kv_cache`` (include/flexattn.h)."""
+    _fields_ = [("page_table", _pi32), ("page_size", _i32), ("max_pages", _i32), ("num_pages", _i32),
+                ("kv_lens", _pi32)]
+
+
+EXPORTED = ("fa_fwd", "fa_fwd_splitkv", "fa_fwd_splitkv_workspace_bytes", "fa_fwd_kvcache",
+            "fa_fwd_kvcache_workspace_bytes", "fa_bwd", "fa_bwd_workspace_bytes",
             "fa_bwd_noalloc", "fa_bwd_noalloc_max_rows", "fa_bwd_preprocess", "fa_bwd_dkdv", "fa_bwd_dq",
             "fa_mask_build_workspace_bytes", "fa_build_block_mask", "fa_strerror", "fa_abi_version",
             "fa_mods_compile", "fa_mods_free_blob", "fa_mods_load", "fa_mods_unload", "fa_mods_fwd", "fa_mods_bwd",
@@ -91,6 +98,11 @@ def load():
     lib.fa_fwd_splitkv.restype = ctypes.c_int
     lib.fa_fwd_splitkv_workspace_bytes.argtypes = [P, ctypes.c_int]
     lib.fa_fwd_splitkv_workspace_bytes.restype = ctypes.c_size_t
+    KV = ctypes.POINTER(FaKvCache)
+    lib.fa_fwd_kvcache.argtypes = [P, KV, v, v, v, v, v, ctypes.c_int, v, ctypes.c_size_t, v]
+    lib.fa_fwd_kvcache.restype = ctypes.c_int
+    lib.fa_fwd_kvcache_workspace_bytes.argtypes = [P, KV, ctypes.c_int]
+    lib.fa_fwd_kvcache_workspace_bytes.restype = ctypes.c_size_t
     lib.fa_bwd.argtypes = [P, v, v, v, v, v, v, v, v, v, v, ctypes.c_size_t, v]
     lib.fa_bwd.restype = ctypes.c_int
     lib.fa_bwd_noalloc.argtypes = [P, v, v, v, v, v, v, v, v, v, v]

@@ -31,7 +31,7 @@ from . import _lib, lowering
 from .block_mask import BlockMask, _finish, create_block_mask
 from .kernel_tuner import (DEFAULT_BLOCK_C, DEFAULT_BLOCK_R, DEFAULT_NUM_STAGES, DEFAULT_NUM_WARPS,
                            kernel_tiles, tuned_tiles)
-from .mask_mod import MaskSpec, MaskMod
+from .mask_mod import MaskSpec, MaskMod, and_masks, causal_mask, document_ids_mask
 from .score_mod import ScoreSpec
 
 # Granularity of the block tables built internally: a multiple of every
@@ -629,38 +629,149 @@ def flash_attention(q, k, v, mask_mod: Optional[MaskMod] = None, block_r: int = 
 
 def flex_decode(query, key, value, score_mod: Optional[ScoreSpec] = None, block_mask: Optional[BlockMask] = None,
                 scale: Optional[float] = None, enable_gqa: bool = False, num_splits: Optional[int] = None,
-                return_lse: bool = False):
+                return_lse: bool = False, kv_lens=None, page_table=None, kv_len: Optional[int] = None):
     """Forward-only FlexAttention for short query blocks against long key
-    sequences (decoding): the keys of each query tile are split into
+    sequences (decoding).  The keys of each query tile are split into
     ``num_splits`` ranges computed by separate workgroups and merged by their
-    log-sum-exp (C ABI ``fa_fwd_splitkv``; ``None`` picks about two workgroups
-    per CU).  Same results as :func:`flex_attention`'s forward; no gradient.
-    The reference has no decode kernel (it is on its roadmap)."""
+    log-sum-exp (``None`` picks about two workgroups per CU); with grouped-query
+    attention the query heads sharing a kv head run as one tile, so each K / V
+    tile is read once per group.  Same results as :func:`flex_attention`'s
+    forward; no gradient.  The reference has no decode kernel (it is on its
+    roadmap).
+
+    KV cache: ``kv_lens`` (B,) int gives each batch row's key count (keys past
+    it are ignored).  With ``page_table`` (B, max_pages) int, ``key`` / ``value``
+    are paged caches of shape (num_pages, Hkv, page_size, D): key t of batch row
+    b is row t % page_size of page page_table[b, t // page_size] (page_size a
+    multiple of 64); ``kv_len`` is the logical key capacity (default
+    max_pages * page_size) that masks and block masks refer to."""
     torch = _torch()
-    if query.shape[1] != key.shape[1] and not enable_gqa:
-        raise ValueError("query and key head counts differ: pass enable_gqa=True for grouped-query attention")
     mask_mod = None
     if block_mask is not None:
         mask_mod = block_mask.mask_mod
         if not block_mask.has_tables:
             raise ValueError("block_mask has no kernel tables (build it with create_block_mask)")
     mask, score, mods = _resolve(mask_mod, score_mod)
+    paged = page_table is not None
     if mods is not None:  # user mods: the run-time compiled forward, unsplit
+        if paged or kv_lens is not None:
+            raise NotImplementedError("user score / mask callables with a KV cache: pass contiguous keys")
         o, lse, _ = _fwd_core(query, key, value, mask, score, scale, block_mask, None, mods)
         return (o, lse) if return_lse else o
     q, k, v = _dense16(query), _dense16(key), _dense16(value)
-    _check_inputs(q, k, v)
+    if paged:
+        if k.dim() != 4 or k.shape != v.shape:
+            raise ValueError("paged key / value caches must be (num_pages, Hkv, page_size, D)")
+        num_pages, Hkv, page_size, D = k.shape
+        pt = page_table.to(device=q.device, dtype=torch.int32).contiguous()
+        if pt.dim() != 2 or pt.shape[0] != q.shape[0]:
+            raise ValueError("page_table must be (B, max_pages)")
+        Skv = int(kv_len) if kv_len is not None else pt.shape[1] * page_size
+        if q.dim() != 4 or not (q.is_cuda and k.is_cuda and v.is_cuda):
+            raise ValueError("query must be (B, Hq, Sq, D) and all tensors on the GPU")
+        if q.dtype != k.dtype or q.dtype != v.dtype:
+            raise TypeError("query and caches must share a dtype")
+        if q.shape[3] != D or q.shape[1] % Hkv:
+            raise ValueError("head dim or head counts of query and caches do not match")
+    else:
+        _check_inputs(q, k, v)
+        Skv = k.shape[2]
+    if query.shape[1] != (k.shape[1] if paged else key.shape[1]) and not enable_gqa:
+        raise ValueError("query and key head counts differ: pass enable_gqa=True for grouped-query attention")
     _, dname = _dtype_code(q)
-    plan = _get_plan(q, k, mask, score, scale, block_mask, (128, 64 if dname == "bf16" else 32))
+    shape_k = _ShapeOnly((q.shape[0], k.shape[1], Skv, q.shape[3]), q.device, q.dtype) if paged else k
+    plan = _get_plan(q, shape_k, mask, score, scale, block_mask, (128, 64 if dname == "bf16" else 32))
     o = torch.empty_like(q)
     lse = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
     lib = _lib.load()
     n = 0 if num_splits is None else int(num_splits)
-    ws_bytes = lib.fa_fwd_splitkv_workspace_bytes(plan.ptr(), n)
-    ws = torch.empty(max(ws_bytes, 256), device=q.device, dtype=torch.uint8)
-    _lib.check(lib.fa_fwd_splitkv(plan.ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-                                  lse.data_ptr(), n, ws.data_ptr(), ws_bytes, _stream()))
+    if paged or kv_lens is not None:
+        import ctypes
+        kvc = _lib.FaKvCache()
+        keep = []
+        if kv_lens is not None:
+            kl = torch.as_tensor(kv_lens, device=q.device).to(torch.int32).contiguous()
+            if kl.shape != (q.shape[0],):
+                raise ValueError("kv_lens must have one entry per batch row")
+            keep.append(kl)
+            kvc.kv_lens = kl.data_ptr()
+        if paged:
+            keep.append(pt)
+            kvc.page_table, kvc.page_size, kvc.max_pages, kvc.num_pages = pt.data_ptr(), page_size, pt.shape[1], \
+                num_pages
+        ws_bytes = lib.fa_fwd_kvcache_workspace_bytes(plan.ptr(), ctypes.byref(kvc), n)
+        ws = torch.empty(max(ws_bytes, 256), device=q.device, dtype=torch.uint8)
+        _lib.check(lib.fa_fwd_kvcache(plan.ptr(), ctypes.byref(kvc), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                      o.data_ptr(), lse.data_ptr(), n, ws.data_ptr(), ws_bytes, _stream()))
+    else:
+        ws_bytes = lib.fa_fwd_splitkv_workspace_bytes(plan.ptr(), n)
+        ws = torch.empty(max(ws_bytes, 256), device=q.device, dtype=torch.uint8)
+        _lib.check(lib.fa_fwd_splitkv(plan.ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                      lse.data_ptr(), n, ws.data_ptr(), ws_bytes, _stream()))
     return (o, lse) if return_lse else o
+
+
+def _seq_tokens(cu):
+    """Per-token (sequence index, sequence start, sequence length) of packed sequences."""
+    cu = np.asarray(cu, dtype=np.int64).reshape(-1)
+    if cu.size < 2 or cu[0] != 0 or np.any(np.diff(cu) < 0):
+        raise ValueError("cu_seqlens must start at 0 and be non-decreasing")
+    lens = np.diff(cu)
+    seq = np.repeat(np.arange(lens.size), lens)
+    return seq, cu[:-1][seq], lens[seq], cu
+
+
+def varlen_mask(cu_seqlens_q, cu_seqlens_k, causal: bool = False):
+    """Mask mod of packed variable-length sequences (the FlashAttention
+    ``cu_seqlens`` convention): query i of sequence s sees the keys of sequence
+    s, and with ``causal`` only those at most as far from the end of the
+    sequence's keys as the query is from the end of its queries (bottom-right
+    aligned, as in FlashAttention's varlen causal mask).  Equal query and key
+    packings give a document mask (interval kernels); otherwise the mask is a
+    traced callable over per-token index tables."""
+    sq, stq, lq, cq = _seq_tokens(cu_seqlens_q)
+    sk, stk, lk, ck = _seq_tokens(cu_seqlens_k)
+    if cq.size != ck.size:
+        raise ValueError("cu_seqlens_q and cu_seqlens_k must describe the same number of sequences")
+    if np.array_equal(cq, ck):
+        docs = document_ids_mask(sq.astype(np.int32))
+        return and_masks(docs, causal_mask) if causal else docs
+    import torch
+    seq_q, seq_k = torch.from_numpy(sq.astype(np.int32)), torch.from_numpy(sk.astype(np.int32))
+    # causal reach of query i: its key-side position may be at most off_q[i]
+    off_q = torch.from_numpy((np.arange(sq.size) - stq + (np.diff(ck)[sq] - lq)).astype(np.int32))
+    pos_k = torch.from_numpy((np.arange(sk.size) - stk).astype(np.int32))
+
+    def mask(q_idx, kv_idx):
+        same = seq_q[q_idx] == seq_k[kv_idx]
+        return same & (pos_k[kv_idx] <= off_q[q_idx]) if causal else same
+    return mask
+
+
+def flex_attention_varlen(query, key, value, cu_seqlens_q, cu_seqlens_k, causal: bool = False,
+                          score_mod=None, scale: Optional[float] = None, enable_gqa: bool = False,
+                          return_lse: bool = False):
+    """Attention over packed variable-length sequences: query (1, Hq, total_q,
+    D), key / value (1, Hkv, total_k, D), sequence s occupying rows
+    [cu_seqlens_q[s], cu_seqlens_q[s+1]) of the queries and
+    [cu_seqlens_k[s], cu_seqlens_k[s+1]) of the keys (see :func:`varlen_mask`).
+    Differentiable; tokens of different sequences never attend to each other
+    and their tile pairs are skipped."""
+    if query.shape[0] != 1 or key.shape[0] != 1:
+        raise ValueError("packed variable-length inputs have batch size 1: (1, H, total_tokens, D)")
+    mm = varlen_mask(cu_seqlens_q, cu_seqlens_k, causal)
+    bm = create_block_mask(mm, 1, query.shape[1], query.shape[2], key.shape[2], TABLE_BLOCK,
+                           device=query.device if isinstance(mm, MaskSpec) else None)
+    return flex_attention(query, key, value, score_mod=score_mod, block_mask=bm, scale=scale, enable_gqa=enable_gqa,
+                          return_lse=return_lse)
+
+
+class _ShapeOnly:
+    """Stands in for a tensor where only its shape, device and dtype are read
+    (the logical key shape of a paged cache, for the plan)."""
+
+    def __init__(self, shape, device, dtype):
+        self.shape, self.device, self.dtype = tuple(shape), device, dtype
 
 
 def flex_attention(query, key, value, score_mod: Optional[ScoreSpec] = None,
