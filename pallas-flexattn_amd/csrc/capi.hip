@@ -164,7 +164,17 @@ int run_fwd(const FwdArgs& a, hipStream_t s) {
   const int grid = fwd_items(a.p, a.pack, 32 * NW);
   if constexpr (sizeof(T) == 2) {
     if (interval_masks(a.p)) {  // bf16: LDS-DMA + transposing-read kernel
-      hipLaunchKernelGGL((fa::fwd_bf16_kernel<D, BN, NW, M>), dim3(grid * a.n_splits), dim3(NW * 64), 0, s, a);
+      const bool cache = a.pack > 1 || a.page_table || a.kv_lens;
+      if constexpr (NW == 4) {
+        if (cache)
+          hipLaunchKernelGGL((fa::fwd_bf16_kernel<D, BN, NW, M, fa::BuiltinMod, true>), dim3(grid * a.n_splits),
+                             dim3(NW * 64), 0, s, a);
+        else
+          hipLaunchKernelGGL((fa::fwd_bf16_kernel<D, BN, NW, M>), dim3(grid * a.n_splits), dim3(NW * 64), 0, s, a);
+      } else {
+        if (cache) return FA_ERR_UNSUPPORTED;  // the KV-cache variant has 128-row tiles
+        hipLaunchKernelGGL((fa::fwd_bf16_kernel<D, BN, NW, M>), dim3(grid * a.n_splits), dim3(NW * 64), 0, s, a);
+      }
       if (a.n_splits > 1) {
         const size_t n = (size_t)a.p.B * a.p.Hq * a.p.Sq * D;
         hipLaunchKernelGGL((fa::fwd_split_merge<D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
@@ -347,7 +357,7 @@ int device_cus() {
 // inside one mask block.
 int choose_pack(const fa_params* p, const Tiles& t, const Problem& pr) {
   const int g = p->Hq / p->Hkv;
-  if (p->dtype != FA_DTYPE_BF16 || !interval_masks(pr) || g < 2 || p->Sq >= t.bm) return 0;
+  if (p->dtype != FA_DTYPE_BF16 || !interval_masks(pr) || g < 2 || p->Sq >= t.bm || t.bm != 128) return 0;
   if (pr.has_tables && (pr.tab_h != 1 || p->Sq > pr.mblk_q)) return 0;
   return g;
 }
@@ -385,8 +395,8 @@ int fwd_launch(const fa_params* p, const fa_kv_cache* kv, const void* q, const v
   if (!aligned16({q, k, v, o})) return FA_ERR_SHAPE;
   if (a.p.has_tables && (a.p.mblk_q % t.bm || a.p.mblk_kv % t.bn)) return FA_ERR_TABLES;
   if (a.p.has_tables && !a.p.kv_num && !a.p.full_kv_num) return FA_ERR_TABLES;
-  if (kv) {  // paged / per-batch-length keys: the bf16 interval kernel only
-    if (p->dtype != FA_DTYPE_BF16 || !interval_masks(a.p)) return FA_ERR_UNSUPPORTED;
+  if (kv) {  // paged / per-batch-length keys: the bf16 interval kernel, 128-row tiles
+    if (p->dtype != FA_DTYPE_BF16 || !interval_masks(a.p) || t.bm != 128) return FA_ERR_UNSUPPORTED;
     if (kv->page_table) {
       if (kv->page_size < t.bn || kv->page_size % t.bn || kv->num_pages < 1) return FA_ERR_SHAPE;
       if ((long long)kv->max_pages * kv->page_size < p->Skv) return FA_ERR_SHAPE;

@@ -36,7 +36,10 @@
 
 namespace fa {
 
-template <int D, int BN, int NW, bool kMods, class Mod = BuiltinMod>
+// kCache: the KV-cache variant (GQA row packing, paged K / V, per-batch key
+// counts).  Kept out of the plain variant: its per-tile address logic costs
+// the training-shape forward 7 % even when unused (measured A/B).
+template <int D, int BN, int NW, bool kMods, class Mod = BuiltinMod, bool kCache = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(occupancy_for(4 * BN * D * 2, NW, 2))))
 void fwd_bf16_kernel(FwdArgs a) {
   using E = Elt<uint16_t>;
@@ -60,7 +63,7 @@ void fwd_bf16_kernel(FwdArgs a) {
   // A work item's rows: Sq queries of one q head, or with GQA packing the
   // g * Sq rows of a kv head's q heads (contiguous in memory).
   const int g = P.Hq / P.Hkv;
-  const bool pack = a.pack > 1;
+  const bool pack = kCache && a.pack > 1;
   const int rows = pack ? g * P.Sq : P.Sq;
   const int nheads = pack ? P.B * P.Hkv : P.B * P.Hq;
   const int nqt = (rows + BM - 1) / BM;
@@ -75,10 +78,15 @@ void fwd_bf16_kernel(FwdArgs a) {
   const int q0 = qt * BM;
   const int rw = q0 + 32 * w + lr;  // this lane's row of the work item
   const bool qvalid = rw < rows;
-  const int qw = pack ? rw % P.Sq : rw;                           // query position
-  const int h = pack ? hk * g + rw / P.Sq : head - b * P.Hq;      // q head (per lane when packed)
+  const int qw = pack ? rw % P.Sq : rw;  // query position
+  // q head: wave-uniform hu (the group's first head when packed) for the
+  // block-table walk, which must stay scalar; h per lane for score / mask mods
+  const int hu = pack ? hk * g : head - b * P.Hq;
+  const int h = pack ? hu + rw / P.Sq : hu;
   // keys of this batch row
-  const int skv = a.kv_lens ? max(0, min(a.kv_lens[b], P.Skv)) : P.Skv;
+  // (through the scalar cache: the loop bounds and every tile address derive
+  // from it and must stay wave-uniform scalars)
+  const int skv = (kCache && a.kv_lens) ? max(0, min(scalar_load(a.kv_lens, b), P.Skv)) : P.Skv;
 
   const char* kbase_ptr = static_cast<const char*>(a.k) + (size_t)(b * P.Hkv + hk) * P.Skv * RB;
   const char* vbase_ptr = static_cast<const char*>(a.v) + (size_t)(b * P.Hkv + hk) * P.Skv * RB;
@@ -137,7 +145,7 @@ void fwd_bf16_kernel(FwdArgs a) {
   if (P.has_tables) {
     // packed rows share table row 0 of their batch row (the host packs only
     // with tables broadcast over heads and Sq within one mask block)
-    const int row = pack ? tab_row(P, b, 0, 0, P.n_qblk) : tab_row(P, b, h, q0 / P.mblk_q, P.n_qblk);
+    const int row = tab_row(P, b, hu, pack ? 0 : q0 / P.mblk_q, P.n_qblk);
     if (P.full_kv_num) {
       walk.nfull = clamp_count(scalar_load(P.full_kv_num, row), P.kv_width);
       walk.full = P.full_kv_idx + (size_t)row * P.kv_width;
@@ -155,7 +163,7 @@ void fwd_bf16_kernel(FwdArgs a) {
     const char* kp = kbase_ptr + (size_t)kb * RB;
     const char* vp = vbase_ptr + (size_t)kb * RB;
     uint32_t range = (uint32_t)(skv - kb) * RB;
-    if (a.page_table) {  // the tile lies inside one page (page_size is a multiple of BN)
+    if (kCache && a.page_table) {  // the tile lies inside one page (page_size is a multiple of BN)
       const int pg = kb / a.page_size, off = kb - pg * a.page_size;
       const int phys = kb < skv ? scalar_load(a.page_table + (size_t)b * a.max_pages, pg) : -1;
       const bool ok = phys >= 0 && phys < a.num_pages;  // a bad page id reads zeros
