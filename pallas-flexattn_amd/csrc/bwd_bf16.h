@@ -133,6 +133,20 @@ __device__ __forceinline__ void mma_rows2(const RowTile<D>& rt, const char* ta, 
   }
 }
 
+// Steps it = from .. to - 1 of a double-buffered tile walk, the buffer of
+// step it being it & 1, passed as a compile-time constant so that LDS
+// operand addresses fold into immediate offsets: steps run in pairs.
+template <class Step, class Masked>
+__device__ __forceinline__ void run_tiles(int from, int to, Step& step, Masked masked_c) {
+  int it = from;
+  if ((it & 1) && it < to) step(it++, masked_c, Bool<1>{});
+  for (; it + 1 < to; it += 2) {
+    step(it, masked_c, Bool<0>{});
+    step(it + 1, masked_c, Bool<1>{});
+  }
+  if (it < to) step(it, masked_c, Bool<0>{});
+}
+
 __device__ __forceinline__ void zero(f32x16& x) {
 #pragma unroll
   for (int e = 0; e < 16; ++e) x[e] = 0.f;
@@ -299,6 +313,8 @@ void dq_bf16_kernel(BwdArgs a) {
   // complete on every path into the loop
   wait_vmem();
   __syncthreads();
+  // (the buffer index stays a run-time value here: as a constant it costs
+  // this 256-VGPR kernel spills)
   auto step = [&](int it, auto masked_c) {
     const int buf = it & 1;
     const int kbase = kb_next;
@@ -647,8 +663,8 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int s = 0; s < KSTEPS; ++s) vf[s] ^= 0x80008000u;
-  auto step = [&](int it, auto masked_c) {
-    const int buf = it & 1;
+  auto step = [&](int it, auto masked_c, auto buf_c) {
+    constexpr int buf = decltype(buf_c)::value;  // == it & 1, a constant (immediate LDS offsets)
     const int hq = hq_next, qbase = qb_next;
     // past the last tile the copies target qb = Sq (zeros into the idle buffer)
     if (it + 1 < n_it) {
@@ -677,9 +693,8 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
     __syncthreads();
   };
   const int n_full = walk.count_full();
-  int it = 0;
-  for (; it < n_full; ++it) step(it, False{});
-  for (; it < n_it; ++it) step(it, True{});
+  run_tiles(0, n_full, step, False{});
+  run_tiles(n_full, n_it, step, True{});
 
 #pragma unroll
   for (int i = 0; i < DT; ++i) {

@@ -269,15 +269,18 @@ void fwd_bf16_kernel(FwdArgs a) {
   TileRef ref_next{0, 0, 0};
   if (it0 < it1) {
     kb_next = walk.kbase(walk.fetch(it0));
-    issue(kb_next, it0 & 1);
+    issue(kb_next, 0);
     if (it0 + 1 < it1) ref_next = walk.fetch(it0 + 1);
   }
   // unconditional, so the wait-count analysis sees the register loads above
   // complete on every path into the loop
   wait_vmem();
   __syncthreads();
-  for (int it = it0; it < it1; ++it) {
-    const int buf = it & 1;
+  // One tile; buf_c (the LDS buffer the tile sits in) is a compile-time
+  // constant, so every LDS operand address is a per-lane register plus an
+  // immediate offset (the loop below runs tiles in pairs).
+  auto tile_step = [&](int it, auto buf_c) {
+    constexpr int buf = decltype(buf_c)::value;
     const int kbase = kb_next;
     bool masked = it >= n_full;
     if (it + 1 < it1) {
@@ -370,7 +373,13 @@ void fwd_bf16_kernel(FwdArgs a) {
     }
     wait_vmem();
     __syncthreads();
+  };
+  int it = it0;
+  for (; it + 1 < it1; it += 2) {
+    tile_step(it, Bool<0>{});
+    tile_step(it + 1, Bool<1>{});
   }
+  if (it < it1) tile_step(it, Bool<0>{});
 
 #pragma unroll
   for (int i = 0; i < DT; ++i) mfma_drain<FA_FWD_OREG>(oacc[i]);
