@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 1
+#define FA_ABI_VERSION 2
 
 enum fa_dtype { FA_DTYPE_BF16 = 0, FA_DTYPE_F32 = 1 };
 
@@ -82,8 +82,17 @@ typedef struct fa_params {
   int32_t abi_version; /* FA_ABI_VERSION */
   int32_t dtype;       /* enum fa_dtype: q, k, v, o, do, dq, dk, dv */
   int32_t B, Hq, Hkv, Sq, Skv, D;
-  int32_t block_m, block_n; /* kernel tiles; 0 = library default */
-  float scale;              /* softmax scale; 0 = 1/sqrt(D) */
+  /* Kernel tiles, 0 = library default.  block_m (query rows per forward /
+   * dQ workgroup, 32 per wave) x block_n (keys per LDS tile):
+   *   bf16: 128 x 64 (default), 64 x 64; for D >= 64 also 128 x 32,
+   *         128 x 128 and 256 x 64 (8 waves)
+   *   fp32: 128 x 32 (default), 64 x 32
+   * block_kv: keys per dK/dV workgroup (32 per wave): 128 (default), or
+   * 64 for bf16 with D >= 64.  The kernels for document labels without
+   * doc_start (and fp32) run their own tiles: block_m capped at 128,
+   * block_n and block_kv at their defaults. */
+  int32_t block_m, block_n, block_kv;
+  float scale; /* softmax scale; 0 = 1/sqrt(D) */
   int32_t window_left, window_right;
   const int32_t *q_doc_ids;  /* (B, Sq) or NULL */
   const int32_t *kv_doc_ids; /* (B, Skv) or NULL (required iff q_doc_ids) */

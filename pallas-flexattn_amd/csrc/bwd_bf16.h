@@ -165,6 +165,7 @@ void dq_bf16_kernel(BwdArgs a) {
   constexpr int DT = D / 32;
   constexpr int NC = BN / 16;
   constexpr int TILE = BN * RB;
+  static_assert(4 * BN >= BM, "dQ rows staged through the K / V buffers");
   __shared__ __attribute__((aligned(1024))) char lds[4 * TILE];  // K0 K1 V0 V1
 
   const Problem& P = a.p;
@@ -417,16 +418,17 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   // time; four waves issuing all of theirs at once after a barrier queue for
   // hundreds of cycles).  A tile at qb >= Sq copies zeros.
   // The LSE and Delta tiles go through a register (one value per lane):
-  // waves 0, 1 load LSE and store -LSE * log2(e) later in the step
-  // (stat_store), so the exponent needs one FMA per element; waves 2, 3 load
-  // and store Delta.  The choice is a wave-uniform select, not a branch, and
-  // each pair of waves writes identical data.
+  // waves 0, 1 (wave 0 of a 2-wave group) load LSE and store -LSE * log2(e)
+  // later in the step (stat_store), so the exponent needs one FMA per
+  // element; waves 2, 3 (wave 1) load and store Delta.  The choice is a
+  // wave-uniform select, not a branch, and waves with the same role write
+  // identical data.
   struct TileCopy {
     i32x4 rq, rdo, rst;
     int buf;
   };
   constexpr int NDMA = 2 * TileDma<D, BQ, NW>::IPW + 1;
-  const bool stat_delta = (w & 2) != 0;
+  const bool stat_delta = (w & (NW >= 4 ? 2 : 1)) != 0;
   const float stat_scale = stat_delta ? 1.0f : -kLog2e;
   auto plan = [&](int hq, int qb, int buf) {
     const size_t hoff = (size_t)(b * P.Hq + hq) * P.Sq;
@@ -482,6 +484,7 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
                        const float* dltl, auto&& copy_k, auto&& stat_k, auto masked_c) {
     constexpr bool kMasked = decltype(masked_c)::value;
     constexpr int KS = KSTEPS, NSTEP = 4 * KS, PF = APF, R = PF + 1;
+    static_assert(NDMA + 1 < NSTEP, "the next tile's copies fit the steps before its LSE store");
     static_assert(2 * DT == KS && NQS == 2, "fast path shape");
     // Partial tiles: element e of sub-tile j is query qbase + 32 j + 8 hh +
     // r(e), r(e) = acc_row(e, 0) < 24.  rmask[j] has bit r set iff that query

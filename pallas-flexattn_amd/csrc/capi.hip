@@ -11,9 +11,7 @@
 #include <vector>
 
 #include "../../include/flexattn.h"
-#include "bwd.h"
-#include "bwd_bf16.h"
-#include "fwd_bf16.h"
+#include "launch.h"
 #include "mask_build.h"
 
 // Kernels compiled at run time for one set of user mods (user_mods.h),
@@ -27,32 +25,42 @@ struct fa_mods {
 namespace {
 
 using fa::BwdArgs;
+using fa::cdiv;
 using fa::FwdArgs;
+using fa::fwd_items;
+using fa::interval_masks;
+using fa::launch_status;
 using fa::Problem;
+using fa::Tiles;
 
-struct Tiles {
-  int bm, bn;    // forward / dQ: query tile, key tile
-  int bkv, bq;   // dK/dV: key tile, query tile
-};
-
+// The tiles of a call: the requested ones (0 = default) where an
+// instantiation exists.  bf16 interval kernels: (bm, bn) in {(128, 64),
+// (64, 64)} and, for D >= 64, {(128, 32), (128, 128), (256, 64)}; dK/dV key
+// tile bkv 128, or 64 for D >= 64.  The generic kernels (document labels
+// compared per element; every fp32 call) keep their own tiles: bm at most
+// 128, bn and bkv at the defaults.
 int default_tiles(const fa_params* p, Tiles* t) {
+  t->bm = p->block_m ? p->block_m : 128;
+  t->bkv = p->block_kv ? p->block_kv : 128;
   if (p->dtype == FA_DTYPE_BF16) {
-    t->bm = p->block_m ? p->block_m : 128;
     t->bn = p->block_n ? p->block_n : 64;
-    t->bkv = 128;
     t->bq = 64;
-    if (!((t->bm == 128 || t->bm == 64) && t->bn == 64)) return FA_ERR_UNSUPPORTED;
+    if (p->q_doc_ids && !p->doc_start) {  // generic kernel
+      if (t->bm == 256) t->bm = 128;
+      t->bn = 64;
+      t->bkv = 128;
+    }
+    const bool base = (t->bm == 128 || t->bm == 64) && t->bn == 64;
+    const bool wide = (t->bm == 128 && (t->bn == 32 || t->bn == 128)) || (t->bm == 256 && t->bn == 64);
+    if (!(base || (wide && p->D >= 64))) return FA_ERR_UNSUPPORTED;
+    if (!(t->bkv == 128 || (t->bkv == 64 && p->D >= 64))) return FA_ERR_UNSUPPORTED;
   } else {
-    t->bm = p->block_m ? p->block_m : 128;
     t->bn = p->block_n ? p->block_n : 32;
-    t->bkv = 128;
     t->bq = 32;
-    if (!((t->bm == 128 || t->bm == 64) && t->bn == 32)) return FA_ERR_UNSUPPORTED;
+    if (!((t->bm == 128 || t->bm == 64) && t->bn == 32 && t->bkv == 128)) return FA_ERR_UNSUPPORTED;
   }
   return FA_OK;
 }
-
-inline int cdiv(int a, int b) { return (a + b - 1) / b; }
 
 // Byte budgets of a head group: the L2 of one XCD is 4 MiB; q-tile walks
 // (forward, dQ) measured best at twice that (the misses hit the MALL and the
@@ -139,8 +147,6 @@ int build_problem(const fa_params* p, const Tiles& t, Problem* pr) {
   return FA_OK;
 }
 
-int launch_status() { return hipGetLastError() == hipSuccess ? FA_OK : FA_ERR_LAUNCH; }
-
 // Tensor rows are read and written 16 bytes per lane.
 bool aligned16(std::initializer_list<const void*> ptrs) {
   for (const void* x : ptrs)
@@ -148,116 +154,35 @@ bool aligned16(std::initializer_list<const void*> ptrs) {
   return true;
 }
 
-// The bf16 LDS-DMA kernels evaluate masks as per-lane intervals (windows and
-// contiguous documents); arbitrary document labels go to the generic kernels.
-bool interval_masks(const Problem& p) { return p.q_doc == nullptr || p.doc_start != nullptr; }
-
 // ------------------------------------------------------------- forward ----
-// Work items of the forward: (batch, q head, query tile), or with GQA row
-// packing (batch, kv head, tile of the group's g * Sq rows).
-int fwd_items(const Problem& p, int pack, int bm) {
-  return pack > 1 ? p.B * p.Hkv * cdiv(pack * p.Sq, bm) : p.B * p.Hq * cdiv(p.Sq, bm);
-}
-
-template <typename T, int D, int BN, int NW, bool M>
-int run_fwd(const FwdArgs& a, hipStream_t s) {
-  const int grid = fwd_items(a.p, a.pack, 32 * NW);
-  if constexpr (sizeof(T) == 2) {
-    if (interval_masks(a.p)) {  // bf16: LDS-DMA + transposing-read kernel
-      const bool cache = a.pack > 1 || a.page_table || a.kv_lens;
-      if constexpr (NW == 4) {
-        if (cache)
-          hipLaunchKernelGGL((fa::fwd_bf16_kernel<D, BN, NW, M, fa::BuiltinMod, true>), dim3(grid * a.n_splits),
-                             dim3(NW * 64), 0, s, a);
-        else
-          hipLaunchKernelGGL((fa::fwd_bf16_kernel<D, BN, NW, M>), dim3(grid * a.n_splits), dim3(NW * 64), 0, s, a);
-      } else {
-        if (cache) return FA_ERR_UNSUPPORTED;  // the KV-cache variant has 128-row tiles
-        hipLaunchKernelGGL((fa::fwd_bf16_kernel<D, BN, NW, M>), dim3(grid * a.n_splits), dim3(NW * 64), 0, s, a);
-      }
-      if (a.n_splits > 1) {
-        const size_t n = (size_t)a.p.B * a.p.Hq * a.p.Sq * D;
-        hipLaunchKernelGGL((fa::fwd_split_merge<D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
-      }
-      return launch_status();
-    }
-  }
-  FwdArgs g = a;  // the generic kernel has no split-KV, packed or paged form
-  g.n_splits = 1;
-  g.pack = 0;
-  hipLaunchKernelGGL((fa::fwd_kernel<T, D, BN, NW, M>), dim3(fwd_items(a.p, 0, 32 * NW)), dim3(NW * 64), 0, s, g);
-  return launch_status();
-}
-
-template <typename T, int D, int BN, bool M>
-int fwd_nw(const FwdArgs& a, int bm, hipStream_t s) {
-  return bm == 64 ? run_fwd<T, D, BN, 2, M>(a, s) : run_fwd<T, D, BN, 4, M>(a, s);
-}
-
-template <typename T, int BN, bool M>
-int fwd_d(const FwdArgs& a, int D, int bm, hipStream_t s) {
+template <typename T, bool M>
+int fwd_d(const FwdArgs& a, int D, const Tiles& t, hipStream_t s) {
   switch (D) {
-    case 32: return fwd_nw<T, 32, BN, M>(a, bm, s);
-    case 64: return fwd_nw<T, 64, BN, M>(a, bm, s);
-    default: return fwd_nw<T, 128, BN, M>(a, bm, s);
+    case 32: return fa::launch_fwd<T, 32, M>(a, t, s);
+    case 64: return fa::launch_fwd<T, 64, M>(a, t, s);
+    default: return fa::launch_fwd<T, 128, M>(a, t, s);
   }
 }
 
 bool has_mods(const Problem& p) { return p.alibi != nullptr || p.softcap > 0.f; }
 
-// ------------------------------------------------------------ backward ----
-template <typename T, int D, int BN, int NW, bool M>
-int run_dq(const BwdArgs& a, hipStream_t s) {
-  const int grid = a.p.B * a.p.Hq * cdiv(a.p.Sq, 32 * NW);
-  if constexpr (sizeof(T) == 2) {
-    if (interval_masks(a.p)) {
-      hipLaunchKernelGGL((fa::dq_bf16_kernel<D, BN, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
-      return launch_status();
-    }
-  }
-  hipLaunchKernelGGL((fa::dq_kernel<T, D, BN, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
-  return launch_status();
-}
-
-template <typename T, int D, int BQ, int NW, bool M>
-int run_dkdv(const BwdArgs& a, hipStream_t s) {
-  const int grid = a.p.B * a.p.Hkv * cdiv(a.p.Skv, 32 * NW);
-  if constexpr (sizeof(T) == 2) {
-    if (interval_masks(a.p)) {
-      hipLaunchKernelGGL((fa::dkdv_bf16_kernel<D, BQ, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
-      return launch_status();
-    }
-  }
-  hipLaunchKernelGGL((fa::dkdv_kernel<T, D, BQ, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
-  return launch_status();
-}
-
-template <typename T, int D>
-int run_delta(const BwdArgs& a, hipStream_t s) {
-  const int nrows = a.p.B * a.p.Hq * a.p.Sq;
-  const int rpb = 256 / (D * (int)sizeof(T) / 16);
-  hipLaunchKernelGGL((fa::delta_kernel<T, D>), dim3(cdiv(nrows, rpb)), dim3(256), 0, s, a, nrows);
-  return launch_status();
-}
-
 enum { kStageDelta = 1, kStageDkdv = 2, kStageDq = 4 };
 
-template <typename T, int D, int BN, int BQ, bool M>
-int bwd_all(const BwdArgs& a, int bm, int stages, hipStream_t s) {
+template <typename T, int D, bool M>
+int bwd_all(const BwdArgs& a, const Tiles& t, int stages, hipStream_t s) {
   int rc = FA_OK;
-  if (stages & kStageDelta) rc = run_delta<T, D>(a, s);
-  if (!rc && (stages & kStageDkdv)) rc = run_dkdv<T, D, BQ, 4, M>(a, s);
-  if (!rc && (stages & kStageDq))
-    rc = bm == 64 ? run_dq<T, D, BN, 2, M>(a, s) : run_dq<T, D, BN, 4, M>(a, s);
+  if (stages & kStageDelta) rc = fa::launch_delta<T, D>(a, s);
+  if (!rc && (stages & kStageDkdv)) rc = fa::launch_dkdv<T, D, M>(a, t, s);
+  if (!rc && (stages & kStageDq)) rc = fa::launch_dq<T, D, M>(a, t, s);
   return rc;
 }
 
-template <typename T, int BN, int BQ, bool M>
-int bwd_d(const BwdArgs& a, int D, int bm, int stages, hipStream_t s) {
+template <typename T, bool M>
+int bwd_d(const BwdArgs& a, int D, const Tiles& t, int stages, hipStream_t s) {
   switch (D) {
-    case 32: return bwd_all<T, 32, BN, BQ, M>(a, bm, stages, s);
-    case 64: return bwd_all<T, 64, BN, BQ, M>(a, bm, stages, s);
-    default: return bwd_all<T, 128, BN, BQ, M>(a, bm, stages, s);
+    case 32: return bwd_all<T, 32, M>(a, t, stages, s);
+    case 64: return bwd_all<T, 64, M>(a, t, stages, s);
+    default: return bwd_all<T, 128, M>(a, t, stages, s);
   }
 }
 
@@ -277,10 +202,8 @@ int bwd_stages(const fa_params* p, BwdArgs& a, int stages, hipStream_t s) {
   }
   const bool m = has_mods(a.p);
   if (p->dtype == FA_DTYPE_BF16)
-    return m ? bwd_d<uint16_t, 64, 64, true>(a, p->D, t.bm, stages, s)
-             : bwd_d<uint16_t, 64, 64, false>(a, p->D, t.bm, stages, s);
-  return m ? bwd_d<float, 32, 32, true>(a, p->D, t.bm, stages, s)
-           : bwd_d<float, 32, 32, false>(a, p->D, t.bm, stages, s);
+    return m ? bwd_d<uint16_t, true>(a, p->D, t, stages, s) : bwd_d<uint16_t, false>(a, p->D, t, stages, s);
+  return m ? bwd_d<float, true>(a, p->D, t, stages, s) : bwd_d<float, false>(a, p->D, t, stages, s);
 }
 
 size_t delta_bytes(const fa_params* p) {
@@ -357,7 +280,8 @@ int device_cus() {
 // inside one mask block.
 int choose_pack(const fa_params* p, const Tiles& t, const Problem& pr) {
   const int g = p->Hq / p->Hkv;
-  if (p->dtype != FA_DTYPE_BF16 || !interval_masks(pr) || g < 2 || p->Sq >= t.bm || t.bm != 128) return 0;
+  if (p->dtype != FA_DTYPE_BF16 || !interval_masks(pr) || g < 2 || p->Sq >= t.bm || t.bm != 128 || t.bn != 64)
+    return 0;
   if (pr.has_tables && (pr.tab_h != 1 || p->Sq > pr.mblk_q)) return 0;
   return g;
 }
@@ -396,7 +320,7 @@ int fwd_launch(const fa_params* p, const fa_kv_cache* kv, const void* q, const v
   if (a.p.has_tables && (a.p.mblk_q % t.bm || a.p.mblk_kv % t.bn)) return FA_ERR_TABLES;
   if (a.p.has_tables && !a.p.kv_num && !a.p.full_kv_num) return FA_ERR_TABLES;
   if (kv) {  // paged / per-batch-length keys: the bf16 interval kernel, 128-row tiles
-    if (p->dtype != FA_DTYPE_BF16 || !interval_masks(a.p) || t.bm != 128) return FA_ERR_UNSUPPORTED;
+    if (p->dtype != FA_DTYPE_BF16 || !interval_masks(a.p) || t.bm != 128 || t.bn != 64) return FA_ERR_UNSUPPORTED;
     if (kv->page_table) {
       if (kv->page_size < t.bn || kv->page_size % t.bn || kv->num_pages < 1) return FA_ERR_SHAPE;
       if ((long long)kv->max_pages * kv->page_size < p->Skv) return FA_ERR_SHAPE;
@@ -422,8 +346,8 @@ int fwd_launch(const fa_params* p, const fa_kv_cache* kv, const void* q, const v
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool m = has_mods(a.p);
   if (p->dtype == FA_DTYPE_BF16)
-    return m ? fwd_d<uint16_t, 64, true>(a, p->D, t.bm, s) : fwd_d<uint16_t, 64, false>(a, p->D, t.bm, s);
-  return m ? fwd_d<float, 32, true>(a, p->D, t.bm, s) : fwd_d<float, 32, false>(a, p->D, t.bm, s);
+    return m ? fwd_d<uint16_t, true>(a, p->D, t, s) : fwd_d<uint16_t, false>(a, p->D, t, s);
+  return m ? fwd_d<float, true>(a, p->D, t, s) : fwd_d<float, false>(a, p->D, t, s);
 }
 
 #include "user_mods.h"
@@ -642,11 +566,11 @@ int mods_bwd_stages(const fa_mods* m, const fa_params* p, const void* const* buf
   }
   if (stages & kStageDelta) {
     if (p->dtype == FA_DTYPE_BF16)
-      rc = p->D == 32 ? run_delta<uint16_t, 32>(a, s) : p->D == 64 ? run_delta<uint16_t, 64>(a, s)
-                                                                    : run_delta<uint16_t, 128>(a, s);
+      rc = p->D == 32 ? fa::launch_delta<uint16_t, 32>(a, s) : p->D == 64 ? fa::launch_delta<uint16_t, 64>(a, s)
+                                                                    : fa::launch_delta<uint16_t, 128>(a, s);
     else
-      rc = p->D == 32 ? run_delta<float, 32>(a, s) : p->D == 64 ? run_delta<float, 64>(a, s)
-                                                                 : run_delta<float, 128>(a, s);
+      rc = p->D == 32 ? fa::launch_delta<float, 32>(a, s) : p->D == 64 ? fa::launch_delta<float, 64>(a, s)
+                                                                 : fa::launch_delta<float, 128>(a, s);
     if (rc) return rc;
   }
   if (stages & kStageDkdv) {

@@ -54,6 +54,7 @@ void fwd_bf16_kernel(FwdArgs a) {
   constexpr int IPW = TILE / 1024 / NW; // DMA instructions per wave per tile
   static_assert(KCH >= 4 && D % 32 == 0 && BN % 32 == 0, "tile shape");
   static_assert(TILE % (1024 * NW) == 0, "DMA split");
+  static_assert(4 * BN >= BM, "O rows staged through the K / V buffers");
 
   __shared__ __attribute__((aligned(1024))) char lds[4 * TILE];  // K0 K1 V0 V1
 
@@ -355,8 +356,11 @@ void fwd_bf16_kernel(FwdArgs a) {
       softmax(sacc, pf);
       // the 2 wait states an MFMA needs after a VALU write of its operand,
       // once for all of P (the PV MFMAs then carry no s_nop)
-      static_assert(BN / 16 == 4 || BN / 16 == 2, "P fragments");
-      if constexpr (BN / 16 == 4)
+      static_assert(BN / 16 == 8 || BN / 16 == 4 || BN / 16 == 2, "P fragments");
+      if constexpr (BN / 16 == 8)
+        asm volatile("s_nop 1" : "+v"(pf[0]), "+v"(pf[1]), "+v"(pf[2]), "+v"(pf[3]), "+v"(pf[4]), "+v"(pf[5]),
+                     "+v"(pf[6]), "+v"(pf[7]));
+      else if constexpr (BN / 16 == 4)
         asm volatile("s_nop 1" : "+v"(pf[0]), "+v"(pf[1]), "+v"(pf[2]), "+v"(pf[3]));
       else
         asm volatile("s_nop 1" : "+v"(pf[0]), "+v"(pf[1]));

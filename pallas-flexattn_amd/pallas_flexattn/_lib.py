@@ -10,7 +10,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 # FLEXATTN_LIB names another build of the same library (same ABI), e.g. to
 # time two builds side by side in one process tree.
 LIB_PATH = os.environ.get("FLEXATTN_LIB") or os.path.join(_HERE, "libflexattn.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_BF16 = 0
 DTYPE_F32 = 1
@@ -25,7 +25,7 @@ class FaParams(ctypes.Structure):
     _fields_ = [
         ("abi_version", _i32), ("dtype", _i32),
         ("B", _i32), ("Hq", _i32), ("Hkv", _i32), ("Sq", _i32), ("Skv", _i32), ("D", _i32),
-        ("block_m", _i32), ("block_n", _i32),
+        ("block_m", _i32), ("block_n", _i32), ("block_kv", _i32),
         ("scale", ctypes.c_float),
         ("window_left", _i32), ("window_right", _i32),
         ("q_doc_ids", _pi32), ("kv_doc_ids", _pi32),

@@ -29,13 +29,14 @@ import numpy as np
 
 from . import _lib, lowering
 from .block_mask import BlockMask, _finish, create_block_mask
-from .kernel_tuner import (DEFAULT_BLOCK_C, DEFAULT_BLOCK_R, DEFAULT_NUM_STAGES, DEFAULT_NUM_WARPS,
+from .kernel_tuner import (DEFAULT_BLOCK_C, DEFAULT_BLOCK_R, DEFAULT_NUM_STAGES, DEFAULT_NUM_WARPS, DEFAULT_TILES,
                            kernel_tiles, tuned_tiles)
 from .mask_mod import MaskSpec, MaskMod, and_masks, causal_mask, document_ids_mask
 from .score_mod import ScoreSpec
 
 # Granularity of the block tables built internally: a multiple of every
-# kernel tile (64/128 queries, 32/64 keys, 128-key dK/dV tiles).
+# kernel tile up to 128 (64/128 queries, 32/64/128 keys, 64/128-key dK/dV
+# tiles); 256-row query tiles get tables at 256.
 TABLE_BLOCK = 128
 
 
@@ -85,7 +86,7 @@ class _Plan:
     so repeated calls make no host-to-device copies."""
 
     def __init__(self, q, k, mask: Optional[MaskSpec], score: Optional[ScoreSpec], scale: Optional[float],
-                 block_mask: Optional[BlockMask], tiles: Tuple[int, int]):
+                 block_mask: Optional[BlockMask], tiles: Tuple[int, int, int]):
         B, Hq, Sq, D = q.shape
         Hkv, Skv = k.shape[1], k.shape[2]
         code, dname = _dtype_code(q)
@@ -93,7 +94,7 @@ class _Plan:
         p.abi_version = _lib.ABI_VERSION
         p.dtype = code
         p.B, p.Hq, p.Hkv, p.Sq, p.Skv, p.D = B, Hq, Hkv, Sq, Skv, D
-        p.block_m, p.block_n = tiles
+        p.block_m, p.block_n, p.block_kv = tiles
         p.scale = 0.0 if scale is None else float(scale)
         p.window_left = p.window_right = -1
         self.keep = []
@@ -119,7 +120,7 @@ class _Plan:
                 raise ValueError(f"block mask built for ({block_mask.q_len}, {block_mask.kv_len}), "
                                  f"inputs are ({Sq}, {Skv})")
             bs = block_mask.block_size
-            if bs % tiles[0] or bs % tiles[1] or bs % 128:
+            if bs % tiles[0] or bs % tiles[1] or bs % tiles[2] or bs % 128:
                 raise ValueError(f"block_size {bs} must be a multiple of 128 and of the kernel tiles {tiles}")
             tb, th = block_mask.table_shape
             if tb not in (1, B) or th not in (1, Hq):
@@ -165,16 +166,17 @@ def _get_plan(q, k, mask, score, scale, block_mask, tiles) -> _Plan:
 _MASK_CACHE = {}
 
 
-def _internal_block_mask(mask: MaskSpec, B: int, Sq: int, Skv: int, device=None) -> BlockMask:
+def _internal_block_mask(mask: MaskSpec, B: int, Sq: int, Skv: int, device=None,
+                         block: int = TABLE_BLOCK) -> BlockMask:
     """Tables for a mask given without a BlockMask, built on ``device`` when it is a GPU."""
     on_gpu = device is not None and getattr(device, "type", str(device)) == "cuda"
-    key = (mask.key(), B, Sq, Skv, str(device) if on_gpu else None)
+    key = (mask.key(), B, Sq, Skv, str(device) if on_gpu else None, block)
     bm = _MASK_CACHE.get(key)
     if bm is None:
         if on_gpu:
-            bm = create_block_mask(mask, B, 1, Sq, Skv, TABLE_BLOCK, device=device)
+            bm = create_block_mask(mask, B, 1, Sq, Skv, block, device=device)
         else:
-            bm = _finish(None, None, mask, B, 1, Sq, Skv, TABLE_BLOCK)
+            bm = _finish(None, None, mask, B, 1, Sq, Skv, block)
         if len(_MASK_CACHE) > 64:
             _MASK_CACHE.clear()
         _MASK_CACHE[key] = bm
@@ -304,27 +306,40 @@ def _mods_args(mods, plan, q, score):
     return _mods_handle(mods, code, q.shape[3], flags, q.device), arr, len(bufs)
 
 
-def _user_block_mask(lmask, B, H, Sq, Skv):
+def _user_block_mask(lmask, B, H, Sq, Skv, block: int = TABLE_BLOCK):
     """Exact tables of a lowered mask at the kernels' table granularity
     (evaluated on the host from the traced expression), cached."""
-    key = ("user", id(lmask), B, H, Sq, Skv)
+    key = ("user", id(lmask), B, H, Sq, Skv, block)
     hit = _MASK_CACHE.get(key)
     if hit is None or hit[0] is not lmask:
         if len(_MASK_CACHE) > 64:
             _MASK_CACHE.clear()
-        hit = _MASK_CACHE[key] = (lmask, create_block_mask(lmask, B, H, Sq, Skv, TABLE_BLOCK))
+        hit = _MASK_CACHE[key] = (lmask, create_block_mask(lmask, B, H, Sq, Skv, block))
     return hit[1]
 
 
-def _tables_for(mask, mods, block_mask, q, k):
-    """The block mask a call walks: the caller's, or one built for its mask."""
+def _tables_for(mask, mods, block_mask, q, k, tiles):
+    """(block mask, tiles) of a call: the caller's tables, or ones built for
+    its mask, at a block size every kernel tile divides: 128, or the query
+    tile when that is larger (256-row tiles).  A caller's tables at another
+    size are re-derived where the mask is known; otherwise the query tile
+    drops to 128 rows."""
+    blk = max(TABLE_BLOCK, tiles[0])
     if block_mask is not None:
-        return block_mask
+        if block_mask.block_size % blk == 0:
+            return block_mask, tiles
+        if mask is not None and not mask.is_trivial:
+            return _internal_block_mask(mask, q.shape[0], q.shape[2], k.shape[2], q.device, blk), tiles
+        if mods is not None and mods.mask is not None:
+            return _user_block_mask(mods.mask, q.shape[0], q.shape[1], q.shape[2], k.shape[2], blk), tiles
+        if tiles[0] > TABLE_BLOCK:
+            return block_mask, (TABLE_BLOCK,) + tuple(tiles[1:])
+        return block_mask, tiles  # the plan reports the mismatch
     if mask is not None and not mask.is_trivial:
-        return _internal_block_mask(mask, q.shape[0], q.shape[2], k.shape[2], q.device)
+        return _internal_block_mask(mask, q.shape[0], q.shape[2], k.shape[2], q.device, blk), tiles
     if mods is not None and mods.mask is not None:
-        return _user_block_mask(mods.mask, q.shape[0], q.shape[1], q.shape[2], k.shape[2])
-    return None
+        return _user_block_mask(mods.mask, q.shape[0], q.shape[1], q.shape[2], k.shape[2], blk), tiles
+    return None, tiles
 
 
 def _stream():
@@ -342,9 +357,9 @@ def _fwd_core(q, k, v, mask, score, scale, block_mask, tiles, mods=None):
     torch = _torch()
     _check_inputs(q, k, v)
     q, k, v = _dense16(q), _dense16(k), _dense16(v)
-    block_mask = _tables_for(mask, mods, block_mask, q, k)
     if mods is not None:
         tiles = _MODS_TILES[_dtype_code(q)[1]]
+    block_mask, tiles = _tables_for(mask, mods, block_mask, q, k, tiles)
     plan = _get_plan(q, k, mask, score, scale, block_mask, tiles)
     o = torch.empty_like(q)
     lse = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
@@ -372,9 +387,9 @@ def _bwd_core(q, k, v, o, lse, do, mask, score, scale, block_mask, tiles, mods=N
     if o.shape != q.shape or do.shape != q.shape or lse.shape != q.shape[:3]:
         raise ValueError("o / do / lse shapes do not match q")
     if plan is None:
-        block_mask = _tables_for(mask, mods, block_mask, q, k)
         if mods is not None:
             tiles = _MODS_TILES[_dtype_code(q)[1]]
+        block_mask, tiles = _tables_for(mask, mods, block_mask, q, k, tiles)
         plan = _get_plan(q, k, mask, score, scale, block_mask, tiles)
     lib = _lib.load()
     ws_bytes = lib.fa_bwd_workspace_bytes(plan.ptr())
@@ -393,7 +408,7 @@ def _bwd_core(q, k, v, o, lse, do, mask, score, scale, block_mask, tiles, mods=N
 
 
 # tiles of the run-time compiled kernels (fixed at compile time)
-_MODS_TILES = {"bf16": (128, 64), "fp32": (128, 32)}
+_MODS_TILES = {"bf16": (128, 64, 128), "fp32": (128, 32, 128)}
 
 
 def _sparse(mask) -> bool:
@@ -415,9 +430,9 @@ def _as4d(t):
 def _stage_plan(q4, k4, mask_mod, block_r, block_c, scale=None):
     """(plan, user mods) of a reference-signature backward stage."""
     mask, _, mods = _resolve(mask_mod, None)
-    bm = _tables_for(mask, mods, None, q4, k4)
     tiles = _MODS_TILES[_dtype_code(q4)[1]] if mods is not None else \
-        _ref_tiles(q4, block_r, block_c, bm is not None)
+        _ref_tiles(q4, block_r, block_c, _sparse(mask) or (mods is not None and mods.mask is not None))
+    bm, tiles = _tables_for(mask, mods, None, q4, k4, tiles)
     return _get_plan(q4, k4, mask, None, scale, bm, tiles), mods
 
 
@@ -504,10 +519,11 @@ class Runner:
         if mods is not None:
             raise NotImplementedError("Runner takes the built-in mask / score descriptors; use flex_attention for "
                                       "user callables")
-        if block_mask is None and mask is not None and not mask.is_trivial:
-            block_mask = _internal_block_mask(mask, q.shape[0], q.shape[2], k.shape[2], q.device)
         _, dname = _dtype_code(q)
-        tiles = tiles or (128, 64 if dname == "bf16" else 32)
+        tiles = tuple(tiles or DEFAULT_TILES[dname])
+        if len(tiles) == 2:
+            tiles = tiles + (DEFAULT_TILES[dname][2],)
+        block_mask, tiles = _tables_for(mask, None, block_mask, self.q, self.k, tiles)
         self.plan = _Plan(self.q, self.k, mask, score, scale, block_mask, tiles)
         self.block_mask = block_mask
         self.o = torch.empty_like(self.q)
@@ -680,7 +696,7 @@ def flex_decode(query, key, value, score_mod: Optional[ScoreSpec] = None, block_
         raise ValueError("query and key head counts differ: pass enable_gqa=True for grouped-query attention")
     _, dname = _dtype_code(q)
     shape_k = _ShapeOnly((q.shape[0], k.shape[1], Skv, q.shape[3]), q.device, q.dtype) if paged else k
-    plan = _get_plan(q, shape_k, mask, score, scale, block_mask, (128, 64 if dname == "bf16" else 32))
+    plan = _get_plan(q, shape_k, mask, score, scale, block_mask, DEFAULT_TILES[dname])
     o = torch.empty_like(q)
     lse = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
     lib = _lib.load()
@@ -780,8 +796,10 @@ def flex_attention(query, key, value, score_mod: Optional[ScoreSpec] = None,
     """FlexAttention: ``softmax(mask(score_mod(scale * q k^T))) v`` over the
     blocks of ``block_mask`` (all blocks when None).  Differentiable.
 
-    ``kernel_options`` may set ``BLOCK_M`` / ``BLOCK_N``; otherwise a tuned
-    table entry or the defaults (bf16: 128 x 64, fp32: 128 x 32) are used."""
+    ``kernel_options`` may set ``BLOCK_M`` (query rows per forward / dQ
+    workgroup, 32 per wave), ``BLOCK_N`` (keys per LDS tile) and ``BLOCK_KV``
+    (keys per dK/dV workgroup); otherwise the tuned table entry for the shape
+    class or the defaults (bf16: 128 x 64 / 128, fp32: 128 x 32 / 128) run."""
     if query.shape[1] != key.shape[1] and not enable_gqa:
         raise ValueError("query and key head counts differ: pass enable_gqa=True for grouped-query attention")
     mask_mod = None
@@ -790,20 +808,12 @@ def flex_attention(query, key, value, score_mod: Optional[ScoreSpec] = None,
         if not block_mask.has_tables:
             raise ValueError("block_mask has no kernel tables (build it with create_block_mask)")
     mask, score, mods = _resolve(mask_mod, score_mod)
-    if block_mask is not None and block_mask.block_size % TABLE_BLOCK:
-        # the dK/dV kernel walks 128-key tiles: re-derive the exact tables at 128
-        if mask is not None:
-            block_mask = _internal_block_mask(mask, query.shape[0], query.shape[2], key.shape[2], query.device)
-        elif mods is not None and mods.mask is not None:
-            block_mask = _user_block_mask(mods.mask, query.shape[0], query.shape[1], query.shape[2], key.shape[2])
+    # tables at another block size are re-derived for the kernel tiles (_tables_for)
     _, dname = _dtype_code(query)
     opts = kernel_options or {}
-    tiles = None
-    if "BLOCK_M" in opts or "BLOCK_N" in opts:
-        tiles = (int(opts.get("BLOCK_M", 128)), int(opts.get("BLOCK_N", 64 if dname == "bf16" else 32)))
-    else:
-        tiles = tuned_tiles(query.shape[2], query.shape[3], dname, block_mask is not None) or \
-            (128, 64 if dname == "bf16" else 32)
+    tiles = tuned_tiles(query.shape[2], query.shape[3], dname, block_mask is not None) or DEFAULT_TILES[dname]
+    if any(o in opts for o in ("BLOCK_M", "BLOCK_N", "BLOCK_KV")):
+        tiles = tuple(int(opts.get(o, d)) for o, d in zip(("BLOCK_M", "BLOCK_N", "BLOCK_KV"), DEFAULT_TILES[dname]))
     cfg = (mask, score, scale, block_mask, tiles, mods)
     o, lse = _FlexFn.get().apply(query, key, value, cfg)
     return (o, lse) if return_lse else o

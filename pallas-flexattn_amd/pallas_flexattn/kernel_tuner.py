@@ -3,11 +3,16 @@
 ``get_optimal_params`` / ``get_kernel_config`` / ``print_kernel_config`` keep
 the reference's static table and signatures (``kernel_tuner.py:11-148``).
 Their four numbers are the reference's Triton knobs; :func:`kernel_tiles`
-takes them as hints only: the gfx950 tile of a call (BLOCK_M query rows,
-32 per wave, BLOCK_N keys per LDS tile) is the one :func:`tune` measured
-fastest for the shape class, else the default 128 x 64 (bf16) / 128 x 32
-(fp32).  ``num_warps`` / ``num_stages`` are accepted for signature
-compatibility; the wave count follows BLOCK_M.
+takes them as hints only: the gfx950 tiles of a call are the ones
+:func:`tune` measured fastest for the shape class, else the defaults.  The
+tiles are (BLOCK_M, BLOCK_N, BLOCK_KV): BLOCK_M query rows per forward / dQ
+workgroup (32 per wave, so it sets the wave count: 2, 4 or 8), BLOCK_N keys
+per LDS tile, BLOCK_KV keys per dK/dV workgroup (32 per wave).  The reference's
+``num_warps`` maps onto the waves of BLOCK_M / BLOCK_KV; its ``num_stages``
+(software-pipelining depth) is fixed at two LDS buffers per operand in every
+kernel here: the next tile's copy is issued a whole tile ahead, the kernels
+are not bound by memory latency (HBM at a few percent of its peak, L2 hit
+rates high), and a third buffer would only take LDS that occupancy needs.
 
 :func:`tune` measures the available instantiations on the current GPU and
 stores the winners in a JSON table that ``flex_attention`` consults.
@@ -87,7 +92,8 @@ def print_kernel_config(
 ):
     """Print the configuration (``kernel_tuner.py:104-148``) plus the MI355X tiles it maps to."""
     config = get_kernel_config(batch_size, num_heads, seq_len, head_dim, mask_type)
-    bm, bn = kernel_tiles(config['block_r'], config['block_c'], "bf16")
+    bm, bn, bkv = kernel_tiles(config['block_r'], config['block_c'], "bf16", seq_len, head_dim,
+                               mask_type in ('causal', 'sliding_window'))
     print("=" * 70)
     print("MI355X FlexAttention Kernel Configuration")
     print("=" * 70)
@@ -104,7 +110,8 @@ def print_kernel_config(
     print(f"  BLOCK_C (block_c):      {config['block_c']}")
     print(f"  NUM_WARPS:              {config['num_warps']}")
     print(f"  NUM_STAGES:             {config['num_stages']}")
-    print(f"  gfx950 tiles (bf16):    BLOCK_M={bm} ({bm // 32} waves), BLOCK_N={bn}")
+    print(f"  gfx950 tiles (bf16):    BLOCK_M={bm} ({bm // 32} waves), BLOCK_N={bn}, "
+          f"BLOCK_KV={bkv} ({bkv // 32} waves)")
     print()
     print("Usage:")
     print("  from pallas_flexattn import flash_attention")
@@ -119,19 +126,35 @@ def print_kernel_config(
 
 
 # -- MI355X tile selection ----------------------------------------------------
-SUPPORTED_BLOCK_M = (64, 128)
-SUPPORTED_BLOCK_N = {"bf16": (64,), "fp32": (32,)}
-DEFAULT_TILES = {"bf16": (128, 64), "fp32": (128, 32)}
+SUPPORTED_BLOCK_M = (64, 128, 256)
+SUPPORTED_BLOCK_N = {"bf16": (32, 64, 128), "fp32": (32,)}
+SUPPORTED_BLOCK_KV = {"bf16": (64, 128), "fp32": (128,)}
+DEFAULT_TILES = {"bf16": (128, 64, 128), "fp32": (128, 32, 128)}
+
+
+def candidate_tiles(dtype: str, head_dim: int) -> Tuple[Tuple[int, int, int], ...]:
+    """Every (BLOCK_M, BLOCK_N, BLOCK_KV) the library has kernels for: bf16
+    (BLOCK_M, BLOCK_N) in 128 x 64, 64 x 64 and, for head dims >= 64,
+    128 x 32, 128 x 128, 256 x 64, each with BLOCK_KV 128 or (D >= 64) 64;
+    fp32 128 x 32 and 64 x 32 with BLOCK_KV 128."""
+    if dtype == "fp32":
+        return ((128, 32, 128), (64, 32, 128))
+    fwd = [(128, 64), (64, 64)]
+    kv = [128]
+    if head_dim >= 64:
+        fwd += [(128, 32), (128, 128), (256, 64)]
+        kv += [64]
+    return tuple((bm, bn, bkv) for bm, bn in fwd for bkv in kv)
 
 
 def kernel_tiles(block_r: int, block_c: int, dtype: str, seq_len: Optional[int] = None,
-                 head_dim: Optional[int] = None, sparse: bool = False) -> Tuple[int, int]:
-    """(BLOCK_M, BLOCK_N) for a call that came with the reference's Triton
-    tile hints ``block_r`` / ``block_c``.  The hints describe a Triton
-    schedule on another GPU, so they do not pick the gfx950 tile: the tile
-    recorded by :func:`tune` for this shape class is used when there is one,
-    else the default (128 queries x 64 keys for bf16, 128 x 32 for fp32),
-    which measured fastest on every shape tuned so far."""
+                 head_dim: Optional[int] = None, sparse: bool = False) -> Tuple[int, int, int]:
+    """(BLOCK_M, BLOCK_N, BLOCK_KV) for a call that came with the reference's
+    Triton tile hints ``block_r`` / ``block_c``.  The hints describe a Triton
+    schedule on another GPU, so they do not pick the gfx950 tiles: the tiles
+    recorded by :func:`tune` for this shape class are used when there are
+    some, else the defaults (128 queries x 64 keys, 128-key dK/dV tiles for
+    bf16; 128 x 32, 128 for fp32)."""
     if seq_len is not None and head_dim is not None:
         t = tuned_tiles(seq_len, head_dim, dtype, sparse)
         if t is not None:
@@ -168,10 +191,10 @@ def table_key(seq_len: int, head_dim: int, dtype: str, sparse: bool) -> str:
     return f"{dtype}/D{head_dim}/S{seq_len}/{'sparse' if sparse else 'dense'}"
 
 
-def tuned_tiles(seq_len: int, head_dim: int, dtype: str, sparse: bool) -> Optional[Tuple[int, int]]:
+def tuned_tiles(seq_len: int, head_dim: int, dtype: str, sparse: bool) -> Optional[Tuple[int, int, int]]:
     """Tiles recorded by :func:`tune` for this shape class, if any."""
     e = load_tune_table().get(table_key(seq_len, head_dim, dtype, sparse))
-    return (e["block_m"], e["block_n"]) if e else None
+    return (e["block_m"], e["block_n"], e.get("block_kv", DEFAULT_TILES[dtype][2])) if e else None
 
 
 def _tune_inputs(batch, heads, seq_len, head_dim, causal, dtype):
@@ -188,14 +211,14 @@ def _tune_inputs(batch, heads, seq_len, head_dim, causal, dtype):
 
 def run_candidate(block_m: int, block_n: int = 64, batch: int = 4, heads: int = 32, seq_len: int = 4096,
                   head_dim: int = 128, causal: bool = True, dtype: str = "bf16", iters: int = 3,
-                  backward: bool = False) -> None:
+                  backward: bool = False, block_kv: int = 128) -> None:
     """Run one tile candidate ``iters`` times (forward, or forward + backward)
     and nothing else: the program rocprofv3 counter passes are taken over
     (MFMA busy cycles, HBM bytes) to compare candidates."""
     import torch
     from .flash_attn import flex_attention
     q, k, v, do, bm_mask = _tune_inputs(batch, heads, seq_len, head_dim, causal, dtype)
-    opts = {"BLOCK_M": block_m, "BLOCK_N": block_n}
+    opts = {"BLOCK_M": block_m, "BLOCK_N": block_n, "BLOCK_KV": block_kv}
     qq, kk, vv = (t.detach().requires_grad_(backward) for t in (q, k, v))
     for _ in range(iters):
         o = flex_attention(qq, kk, vv, block_mask=bm_mask, kernel_options=opts)
@@ -206,12 +229,14 @@ def run_candidate(block_m: int, block_n: int = 64, batch: int = 4, heads: int = 
 
 def tune(batch: int = 4, heads: int = 32, seq_len: int = 4096, head_dim: int = 128, causal: bool = True,
          dtype: str = "bf16", iters: int = 10, path: str = TUNE_TABLE) -> Dict[str, int]:
-    """Time every instantiated (BLOCK_M, BLOCK_N) for this shape on the current
-    GPU with hipEvents -- BLOCK_M = 32 x the waves per workgroup (2 or 4), each
-    wave owning 32 query rows; the K / V tiles are double-buffered in LDS in
-    every candidate -- and record the fastest fwd + bwd in the JSON table,
-    with each candidate's forward and fwd + bwd time and TFLOP/s on the
-    unmasked pairs (fwd 4 D P, fwd + bwd 14 D P per head)."""
+    """Time every instantiated (BLOCK_M, BLOCK_N, BLOCK_KV) for this shape
+    (:func:`candidate_tiles`) on the current GPU with hipEvents and record the
+    fastest forward + backward in the JSON table, with each candidate's
+    forward and fwd + bwd time and TFLOP/s on the unmasked pairs (fwd 4 D P,
+    fwd + bwd 14 D P per head).  The axes: waves per forward / dQ workgroup
+    (BLOCK_M / 32: 2, 4, 8), keys per LDS tile (BLOCK_N: 32, 64, 128), waves
+    per dK/dV workgroup (BLOCK_KV / 32: 2, 4); every candidate double-buffers
+    its tiles in LDS (the stage count is not an axis here)."""
     import torch
     from .flash_attn import flex_attention
     q, k, v, do, bm_mask = _tune_inputs(batch, heads, seq_len, head_dim, causal, dtype)
@@ -233,41 +258,41 @@ def tune(batch: int = 4, heads: int = 32, seq_len: int = 4096, head_dim: int = 1
 
     # every candidate's output is checked against the default tile's before it
     # can be recorded: a tile whose kernel disagrees is skipped, not chosen
-    base_opts = {"BLOCK_M": DEFAULT_TILES[dtype][0], "BLOCK_N": DEFAULT_TILES[dtype][1]}
-    ref = _candidate_outputs(q, k, v, do, bm_mask, base_opts)
+    names = ("BLOCK_M", "BLOCK_N", "BLOCK_KV")
+    ref = _candidate_outputs(q, k, v, do, bm_mask, dict(zip(names, DEFAULT_TILES[dtype])))
     tol = 2e-2 if dtype == "bf16" else 1e-5
     results, rejected = {}, {}
-    for bm in SUPPORTED_BLOCK_M:
-        for bn in SUPPORTED_BLOCK_N[dtype]:
-            opts = {"BLOCK_M": bm, "BLOCK_N": bn}
-            bad = _mismatch(ref, _candidate_outputs(q, k, v, do, bm_mask, opts), tol)
-            if bad:
-                rejected[f"{bm}x{bn}"] = bad
-                continue
-            qq, kk, vv = (t.detach().requires_grad_() for t in (q, k, v))
+    for tiles in candidate_tiles(dtype, head_dim):
+        bm, bn, bkv = tiles
+        opts = dict(zip(names, tiles))
+        bad = _mismatch(ref, _candidate_outputs(q, k, v, do, bm_mask, opts), tol)
+        if bad:
+            rejected["x".join(map(str, tiles))] = bad
+            continue
+        qq, kk, vv = (t.detach().requires_grad_() for t in (q, k, v))
 
-            def fwd_only():
-                with torch.no_grad():
-                    flex_attention(q, k, v, block_mask=bm_mask, kernel_options=opts)
+        def fwd_only():
+            with torch.no_grad():
+                flex_attention(q, k, v, block_mask=bm_mask, kernel_options=opts)
 
-            def fwd_bwd():
-                o = flex_attention(qq, kk, vv, block_mask=bm_mask, kernel_options=opts)
-                o.backward(do)
+        def fwd_bwd():
+            o = flex_attention(qq, kk, vv, block_mask=bm_mask, kernel_options=opts)
+            o.backward(do)
 
-            t_f, t_fb = timed(fwd_only), timed(fwd_bwd)
-            results[(bm, bn)] = {"waves": bm // 32, "lds_buffers": 2, "ms_fwd": round(t_f, 4),
-                                 "ms_fwd_bwd": round(t_fb, 4),
-                                 "tflops_fwd": round(flops_fwd / t_f / 1e9, 1),
-                                 "tflops_fwd_bwd": round(3.5 * flops_fwd / t_fb / 1e9, 1),
-                                 "pct_peak_fwd_bwd": round(100 * 3.5 * flops_fwd / t_fb / 1e9 / peak, 2)}
+        t_f, t_fb = timed(fwd_only), timed(fwd_bwd)
+        results[tiles] = {"waves": bm // 32, "dkdv_waves": bkv // 32, "lds_buffers": 2,
+                          "ms_fwd": round(t_f, 4), "ms_fwd_bwd": round(t_fb, 4),
+                          "tflops_fwd": round(flops_fwd / t_f / 1e9, 1),
+                          "tflops_fwd_bwd": round(3.5 * flops_fwd / t_fb / 1e9, 1),
+                          "pct_peak_fwd_bwd": round(100 * 3.5 * flops_fwd / t_fb / 1e9 / peak, 2)}
     if not results:
-        raise RuntimeError(f"tune: every candidate disagreed with the default tile: {rejected}")
-    (bm, bn), best = min(results.items(), key=lambda kv: kv[1]["ms_fwd_bwd"])
+        raise RuntimeError(f"tune: every candidate disagreed with the default tiles: {rejected}")
+    (bm, bn, bkv), best = min(results.items(), key=lambda kv: kv[1]["ms_fwd_bwd"])
     table = load_tune_table(path)
     key = table_key(seq_len, head_dim, dtype, causal)
-    table[key] = {"block_m": bm, "block_n": bn, "ms_fwd_bwd": best["ms_fwd_bwd"],
+    table[key] = {"block_m": bm, "block_n": bn, "block_kv": bkv, "ms_fwd_bwd": best["ms_fwd_bwd"],
                   "shape": f"B{batch} H{heads} S{seq_len} D{head_dim} {'causal' if causal else 'dense'}",
-                  "candidates": {f"{a}x{b}": r for (a, b), r in results.items()}}
+                  "candidates": {"x".join(map(str, t)): r for t, r in results.items()}}
     if rejected:
         table[key]["rejected"] = rejected
     with open(path, "w") as f:
@@ -302,14 +327,15 @@ if __name__ == "__main__":
     parser.add_argument("--mask-type", type=str, default=None,
                         choices=['causal', 'sliding_window', 'bidirectional'])
     parser.add_argument("--tune", action="store_true", help="measure tiles on this GPU and record them")
-    parser.add_argument("--run-candidate", type=int, default=None, metavar="BLOCK_M",
-                        help="only run this BLOCK_M (for rocprofv3 counter passes)")
+    parser.add_argument("--run-candidate", type=int, nargs=3, default=None, metavar=("BLOCK_M", "BLOCK_N", "BLOCK_KV"),
+                        help="only run these tiles (for rocprofv3 counter passes)")
     parser.add_argument("--backward", action="store_true", help="--run-candidate: forward + backward")
     parser.add_argument("--iters", type=int, default=3)
     args = parser.parse_args()
     if args.run_candidate is not None:
-        run_candidate(args.run_candidate, 64, args.batch_size, args.num_heads, args.seq_len, args.head_dim,
-                      args.mask_type == "causal", iters=args.iters, backward=args.backward)
+        bm, bn, bkv = args.run_candidate
+        run_candidate(bm, bn, args.batch_size, args.num_heads, args.seq_len, args.head_dim,
+                      args.mask_type == "causal", iters=args.iters, backward=args.backward, block_kv=bkv)
     elif args.tune:
         print(tune(args.batch_size, args.num_heads, args.seq_len, args.head_dim, args.mask_type == "causal"))
     else:

@@ -146,12 +146,8 @@ def test_no_early_reads_of_asm_mfma_results(tmp_path):
     sys.path.insert(0, os.path.join(ROOT, "pallas-flexattn_amd"))
     import build as b
     b.write_rtc_sources()
-    flags = [f for f in b.FLAGS if f not in ("-shared", "-fPIC")]
-    out = tmp_path / "capi.s"
-    res = subprocess.run([b.HIPCC, *flags, "--cuda-device-only", "-S", *b.SOURCES, "-o", str(out)],
-                         capture_output=True, text=True)
-    assert res.returncode == 0, res.stderr[-2000:]
-    text = out.read_text()
+    outs, _ = b.compile_units(["--cuda-device-only", "-S"], suffix=".s", out_dir=str(tmp_path))
+    text = "\n".join(open(o).read() for o in outs)
     assert ";;#ASMSTART" in text and "v_mfma" in text
     found = early_touches(text)
     assert not found, "\n".join(f"{k} line {ln}: {ws} wait states: {ins}" for k, ln, ws, ins in found[:20])

@@ -8,7 +8,8 @@ import pytest
 
 from pallas_flexattn import _lib
 
-HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "flexattn.h")
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "flexattn.h")
 
 
 def declared_functions():
@@ -32,11 +33,26 @@ def test_abi_version_and_strerror():
         assert lib.fa_strerror(code) != b"unknown status"
 
 
-def test_params_struct_layout_matches_header():
-    # 12 int32 + float + 2 int32, then pointers (8-byte aligned) ... computed from the header order
-    p = _lib.FaParams
-    assert p.scale.offset == 40 and p.q_doc_ids.offset == 56
-    assert ctypes.sizeof(p) == p.full_q_indices.offset + 8
+@pytest.mark.parametrize("cname,pyname", [("fa_params", "FaParams"), ("fa_mask_build", "FaMaskBuild"),
+                                          ("fa_kv_cache", "FaKvCache")])
+def test_struct_layouts_match_header(cname, pyname, tmp_path):
+    """Every field offset and the size of the ctypes mirrors equal what a C
+    compiler makes of include/flexattn.h."""
+    import shutil
+    import subprocess
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    st = getattr(_lib, pyname)
+    fields = [f[0] for f in st._fields_]
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "flexattn.h"\nint main(void) {\n' +
+                   "".join(f'  printf("%zu\\n", offsetof(struct {cname}, {f}));\n' for f in fields) +
+                   f'  printf("%zu\\n", sizeof(struct {cname}));\n  return 0;\n}}\n')
+    exe = tmp_path / "layout"
+    subprocess.run([cc, "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    assert got == [getattr(st, f).offset for f in fields] + [ctypes.sizeof(st)]
 
 
 def _params(**kw):

@@ -86,7 +86,7 @@ def test_split_kv_workspace_and_counts():
     from pallas_flexattn import _lib
     from pallas_flexattn.flash_attn import _Plan
     q, k, v = _case(1, 4, 4, 1, 8192, 128, 3)
-    plan = _Plan(q, k, None, None, None, None, (128, 64))
+    plan = _Plan(q, k, None, None, None, None, (128, 64, 128))
     lib = _lib.load()
     rows = 1 * 4 * 1
     assert lib.fa_fwd_splitkv_workspace_bytes(plan.ptr(), 8) == 8 * rows * (128 + 2) * 4

@@ -53,21 +53,24 @@ def test_kernel_tile_mapping():
     import json
     import pallas_flexattn.kernel_tuner as kt
     for br, bc in ((128, 64), (64, 64), (32, 32), (256, 128)):
-        assert kernel_tiles(br, bc, "bf16") == (128, 64)
-        assert kernel_tiles(br, bc, "fp32") == (128, 32)
-    assert kernel_tiles(64, 64, "bf16", 12345, 128, True) == (128, 64)  # no entry for this shape
+        assert kernel_tiles(br, bc, "bf16") == (128, 64, 128)
+        assert kernel_tiles(br, bc, "fp32") == (128, 32, 128)
+    assert kernel_tiles(64, 64, "bf16", 12345, 128, True) == (128, 64, 128)  # no entry for this shape
 
 
 def test_kernel_tiles_follow_the_tune_table(tmp_path, monkeypatch):
     import json
     import pallas_flexattn.kernel_tuner as kt
     path = tmp_path / "table.json"
-    path.write_text(json.dumps({kt.table_key(1024, 64, "bf16", True): {"block_m": 64, "block_n": 64}}))
+    path.write_text(json.dumps({kt.table_key(1024, 64, "bf16", True): {"block_m": 64, "block_n": 64},
+                                kt.table_key(2048, 128, "bf16", True): {"block_m": 256, "block_n": 64,
+                                                                        "block_kv": 64}}))
     monkeypatch.setattr(kt, "TUNE_TABLE", str(path))
     monkeypatch.setattr(kt.load_tune_table, "__defaults__", (str(path),))
-    assert kt.kernel_tiles(128, 128, "bf16", 1024, 64, True) == (64, 64)
-    assert kt.kernel_tiles(128, 128, "bf16", 1024, 64, False) == (128, 64)
-    assert kt.tuned_tiles(1024, 64, "bf16", True) == (64, 64)
+    assert kt.kernel_tiles(128, 128, "bf16", 1024, 64, True) == (64, 64, 128)  # entries without block_kv
+    assert kt.kernel_tiles(128, 128, "bf16", 1024, 64, False) == (128, 64, 128)
+    assert kt.tuned_tiles(1024, 64, "bf16", True) == (64, 64, 128)
+    assert kt.tuned_tiles(2048, 128, "bf16", True) == (256, 64, 64)
     # parsed once per modification time
     assert kt.load_tune_table(str(path)) is kt.load_tune_table(str(path))
 
@@ -75,16 +78,29 @@ def test_kernel_tiles_follow_the_tune_table(tmp_path, monkeypatch):
 def test_committed_tune_table_is_consistent():
     """The measured table shipped with the package: every entry names an
     instantiated tile pair and is the fastest fwd + bwd of its candidates."""
-    from pallas_flexattn.kernel_tuner import SUPPORTED_BLOCK_N, load_tune_table, TUNE_TABLE
+    from pallas_flexattn.kernel_tuner import candidate_tiles, load_tune_table, TUNE_TABLE
     import os
     if not os.path.exists(TUNE_TABLE):
         pytest.skip("no tune table")
     table = load_tune_table()
     assert table
     for key, e in table.items():
-        dtype = key.split("/")[0]
-        assert e["block_m"] in SUPPORTED_BLOCK_M and e["block_n"] in SUPPORTED_BLOCK_N[dtype]
+        dtype, d = key.split("/")[:2]
+        tiles = (e["block_m"], e["block_n"], e.get("block_kv", 128))
+        assert tiles in candidate_tiles(dtype, int(d[1:]))
         best = min(e["candidates"].items(), key=lambda kv: kv[1]["ms_fwd_bwd"])[0]
-        assert best == f"{e['block_m']}x{e['block_n']}"
+        assert best in (f"{tiles[0]}x{tiles[1]}", "x".join(map(str, tiles)))
         for c in e["candidates"].values():
             assert c["waves"] * 32 in SUPPORTED_BLOCK_M and c["ms_fwd"] < c["ms_fwd_bwd"]
+
+
+def test_candidate_tiles_cover_the_instantiated_axes():
+    from pallas_flexattn.kernel_tuner import SUPPORTED_BLOCK_KV, SUPPORTED_BLOCK_N, candidate_tiles
+    c = candidate_tiles("bf16", 128)
+    assert {t[0] for t in c} == set(SUPPORTED_BLOCK_M)
+    assert {t[1] for t in c} == set(SUPPORTED_BLOCK_N["bf16"])
+    assert {t[2] for t in c} == set(SUPPORTED_BLOCK_KV["bf16"])
+    assert len(c) == len(set(c)) == 10 and c[0] == (128, 64, 128)
+    # D = 32: the DMA split needs at least 1 KiB per wave and tile
+    assert candidate_tiles("bf16", 32) == ((128, 64, 128), (64, 64, 128))
+    assert candidate_tiles("fp32", 128) == ((128, 32, 128), (64, 32, 128))

@@ -22,7 +22,7 @@ def _run(B, Hq, Hkv, S, D, seed, mask):
     v = torch.randn(B, Hkv, S, D, device="cuda", generator=g).to(torch.bfloat16)
     do = torch.randn(B, Hq, S, D, device="cuda", generator=g).to(torch.bfloat16)
     bm = pf.create_block_mask(mask, B, Hq, S, S, 128) if mask is not None else None
-    o, lse, plan = _fwd_core(q, k, v, mask, None, None, bm, (128, 64))
+    o, lse, plan = _fwd_core(q, k, v, mask, None, None, bm, (128, 64, 128))
     lib = _lib.load()
     outs = []
     for noalloc in (False, True):
