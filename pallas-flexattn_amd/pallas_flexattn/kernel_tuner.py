@@ -228,7 +228,8 @@ def run_candidate(block_m: int, block_n: int = 64, batch: int = 4, heads: int = 
 
 
 def tune(batch: int = 4, heads: int = 32, seq_len: int = 4096, head_dim: int = 128, causal: bool = True,
-         dtype: str = "bf16", iters: int = 10, path: str = TUNE_TABLE) -> Dict[str, int]:
+         dtype: str = "bf16", iters: int = 20, rounds: int = 3, margin: float = 0.01,
+         path: str = TUNE_TABLE) -> Dict[str, int]:
     """Time every instantiated (BLOCK_M, BLOCK_N, BLOCK_KV) for this shape
     (:func:`candidate_tiles`) on the current GPU with hipEvents and record the
     fastest forward + backward in the JSON table, with each candidate's
@@ -236,7 +237,11 @@ def tune(batch: int = 4, heads: int = 32, seq_len: int = 4096, head_dim: int = 1
     fwd + bwd 14 D P per head).  The axes: waves per forward / dQ workgroup
     (BLOCK_M / 32: 2, 4, 8), keys per LDS tile (BLOCK_N: 32, 64, 128), waves
     per dK/dV workgroup (BLOCK_KV / 32: 2, 4); every candidate double-buffers
-    its tiles in LDS (the stage count is not an axis here)."""
+    its tiles in LDS (the stage count is not an axis here).  Each time is the
+    best of ``rounds`` passes over all candidates in turn (``iters`` calls
+    each), so clock and thermal drift does not favour one candidate.  A
+    candidate replaces the default tiles only when it is faster by more than
+    ``margin`` (run-to-run spread on one GPU is about 1 %)."""
     import torch
     from .flash_attn import flex_attention
     q, k, v, do, bm_mask = _tune_inputs(batch, heads, seq_len, head_dim, causal, dtype)
@@ -261,9 +266,8 @@ def tune(batch: int = 4, heads: int = 32, seq_len: int = 4096, head_dim: int = 1
     names = ("BLOCK_M", "BLOCK_N", "BLOCK_KV")
     ref = _candidate_outputs(q, k, v, do, bm_mask, dict(zip(names, DEFAULT_TILES[dtype])))
     tol = 2e-2 if dtype == "bf16" else 1e-5
-    results, rejected = {}, {}
+    runs, rejected = {}, {}
     for tiles in candidate_tiles(dtype, head_dim):
-        bm, bn, bkv = tiles
         opts = dict(zip(names, tiles))
         bad = _mismatch(ref, _candidate_outputs(q, k, v, do, bm_mask, opts), tol)
         if bad:
@@ -271,15 +275,25 @@ def tune(batch: int = 4, heads: int = 32, seq_len: int = 4096, head_dim: int = 1
             continue
         qq, kk, vv = (t.detach().requires_grad_() for t in (q, k, v))
 
-        def fwd_only():
+        def fwd_only(opts=opts):
             with torch.no_grad():
                 flex_attention(q, k, v, block_mask=bm_mask, kernel_options=opts)
 
-        def fwd_bwd():
+        def fwd_bwd(opts=opts, qq=qq, kk=kk, vv=vv):
             o = flex_attention(qq, kk, vv, block_mask=bm_mask, kernel_options=opts)
             o.backward(do)
 
-        t_f, t_fb = timed(fwd_only), timed(fwd_bwd)
+        runs[tiles] = (fwd_only, fwd_bwd)
+    best_f = {t: float("inf") for t in runs}
+    best_fb = dict(best_f)
+    for _ in range(rounds):
+        for tiles, (fwd_only, fwd_bwd) in runs.items():
+            best_f[tiles] = min(best_f[tiles], timed(fwd_only))
+            best_fb[tiles] = min(best_fb[tiles], timed(fwd_bwd))
+    results = {}
+    for tiles in runs:
+        bm, bn, bkv = tiles
+        t_f, t_fb = best_f[tiles], best_fb[tiles]
         results[tiles] = {"waves": bm // 32, "dkdv_waves": bkv // 32, "lds_buffers": 2,
                           "ms_fwd": round(t_f, 4), "ms_fwd_bwd": round(t_fb, 4),
                           "tflops_fwd": round(flops_fwd / t_f / 1e9, 1),
@@ -288,9 +302,12 @@ def tune(batch: int = 4, heads: int = 32, seq_len: int = 4096, head_dim: int = 1
     if not results:
         raise RuntimeError(f"tune: every candidate disagreed with the default tiles: {rejected}")
     (bm, bn, bkv), best = min(results.items(), key=lambda kv: kv[1]["ms_fwd_bwd"])
+    default = results.get(DEFAULT_TILES[dtype])
+    if default is not None and best["ms_fwd_bwd"] > default["ms_fwd_bwd"] * (1.0 - margin):
+        (bm, bn, bkv), best = DEFAULT_TILES[dtype], default
     table = load_tune_table(path)
     key = table_key(seq_len, head_dim, dtype, causal)
-    table[key] = {"block_m": bm, "block_n": bn, "block_kv": bkv, "ms_fwd_bwd": best["ms_fwd_bwd"],
+    table[key] = {"block_m": bm, "block_n": bn, "block_kv": bkv, "ms_fwd_bwd": best["ms_fwd_bwd"], "margin": margin,
                   "shape": f"B{batch} H{heads} S{seq_len} D{head_dim} {'causal' if causal else 'dense'}",
                   "candidates": {"x".join(map(str, t)): r for t, r in results.items()}}
     if rejected:
@@ -330,13 +347,14 @@ if __name__ == "__main__":
     parser.add_argument("--run-candidate", type=int, nargs=3, default=None, metavar=("BLOCK_M", "BLOCK_N", "BLOCK_KV"),
                         help="only run these tiles (for rocprofv3 counter passes)")
     parser.add_argument("--backward", action="store_true", help="--run-candidate: forward + backward")
-    parser.add_argument("--iters", type=int, default=3)
+    parser.add_argument("--iters", type=int, default=None, help="calls per measurement (3 / 20 with --tune)")
     args = parser.parse_args()
     if args.run_candidate is not None:
         bm, bn, bkv = args.run_candidate
         run_candidate(bm, bn, args.batch_size, args.num_heads, args.seq_len, args.head_dim,
-                      args.mask_type == "causal", iters=args.iters, backward=args.backward, block_kv=bkv)
+                      args.mask_type == "causal", iters=args.iters or 3, backward=args.backward, block_kv=bkv)
     elif args.tune:
-        print(tune(args.batch_size, args.num_heads, args.seq_len, args.head_dim, args.mask_type == "causal"))
+        print(tune(args.batch_size, args.num_heads, args.seq_len, args.head_dim, args.mask_type == "causal",
+                   iters=args.iters or 20))
     else:
         print_kernel_config(args.batch_size, args.num_heads, args.seq_len, args.head_dim, args.mask_type)
