@@ -39,7 +39,11 @@ extern "C" {
 
 #define FA_ABI_VERSION 2
 
-enum fa_dtype { FA_DTYPE_BF16 = 0, FA_DTYPE_F32 = 1 };
+enum fa_dtype {
+  FA_DTYPE_BF16 = 0,
+  FA_DTYPE_F32 = 1,
+  FA_DTYPE_FP8_E4M3 = 2 /* fa_fwd_fp8 only: q, k, v OCP e4m3 (fa_fp8_inputs), o bf16 */
+};
 
 enum fa_status {
   FA_OK = 0,
@@ -147,6 +151,34 @@ size_t fa_fwd_kvcache_workspace_bytes(const fa_params *p, const fa_kv_cache *kv,
 int fa_fwd_kvcache(const fa_params *p, const fa_kv_cache *kv, const void *q, const void *k_cache,
                    const void *v_cache, void *o, float *lse, int n_splits, void *workspace, size_t workspace_bytes,
                    void *stream);
+
+/* FP8 forward (p->dtype = FA_DTYPE_FP8_E4M3; D = 64 or 128; 128 x 64 tiles):
+ * Q (B, Hq, Sq, D) and K (B, Hkv, Skv, D) in OCP e4m3, V transposed per kv
+ * head, (B, Hkv, D, v_ld) e4m3 with v_ld a multiple of 128 >= Skv and the
+ * keys past Skv finite (zero, as fa_quantize_fp8 writes them).  Every 128-row
+ * block of a head (queries for Q, keys for K and V) carries one float scale,
+ * a power of two in [2^-126, 2^127]: the tensor's value is element x scale.
+ * Scales are (B * Hq, ceil(Sq / 128)) for Q, (B * Hkv, ceil(Skv / 128)) for K
+ * and V.  Both products run on the scaled fp8 MFMA (S exact in fp32; P
+ * rounded to e4m3 as p * 8).  Masks, block tables and the built-in score mods
+ * as fa_fwd's bf16 path (document labels only as contiguous runs); o is bf16,
+ * lse fp32.  No reference counterpart (its kernels are bf16 / fp32). */
+typedef struct fa_fp8_inputs {
+  const void *q, *k, *vt;
+  int32_t v_ld;
+  const float *q_scale, *k_scale, *v_scale;
+} fa_fp8_inputs;
+int fa_fwd_fp8(const fa_params *p, const fa_fp8_inputs *in, void *o, float *lse, void *stream);
+
+/* bf16 rows -> e4m3 with one power-of-two scale per 128-row block:
+ * x (heads, S, D) bf16; scale (heads, ceil(S / 128)) = 2^e with e the
+ * smallest integer such that 448 2^e >= the block's max |x| (clamped to
+ * [-126, 127]; 1 for an all-zero block), element = RNE(x / scale) in e4m3.
+ * transpose = 0: out (heads, S, D); transpose = 1: out (heads, D, ld) with
+ * ld = 128 * ceil(S / 128) (the V^T operand of fa_fwd_fp8), keys past S
+ * zero.  D = 32, 64 or 128.  No reference counterpart. */
+int fa_quantize_fp8(const void *x, int32_t heads, int32_t S, int32_t D, int32_t transpose, void *out, float *scale,
+                    void *stream);
 
 /* Bytes of device scratch fa_bwd needs for these params. */
 size_t fa_bwd_workspace_bytes(const fa_params *p);

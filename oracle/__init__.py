@@ -26,4 +26,9 @@ would be marked "parity unpinned"; none is):
                     bwd ``:168-407``) with the same bf16 cast points.  Used as the CPU
                     baseline and cross-checked against ``attention``.
 * ``bf16``        — float32 -> bfloat16 round-to-nearest-even in numpy.
+* ``fp8``         — OCP e4m3 codec, the fp8 path's block quantisation and a
+                    model of its P rounding (no reference counterpart: the
+                    reference has no fp8 path).  Pinned against torch's
+                    float8_e4m3fn conversion, closed forms, the quantisation's
+                    defining invariants and ``attention``.
 """

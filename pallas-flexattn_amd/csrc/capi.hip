@@ -54,6 +54,10 @@ int default_tiles(const fa_params* p, Tiles* t) {
     const bool wide = (t->bm == 128 && (t->bn == 32 || t->bn == 128)) || (t->bm == 256 && t->bn == 64);
     if (!(base || (wide && p->D >= 64))) return FA_ERR_UNSUPPORTED;
     if (!(t->bkv == 128 || (t->bkv == 64 && p->D >= 64))) return FA_ERR_UNSUPPORTED;
+  } else if (p->dtype == FA_DTYPE_FP8_E4M3) {  // forward only: 128 x 64
+    t->bn = p->block_n ? p->block_n : 64;
+    t->bq = 64;
+    if (!(t->bm == 128 && t->bn == 64 && t->bkv == 128)) return FA_ERR_UNSUPPORTED;
   } else {
     t->bn = p->block_n ? p->block_n : 32;
     t->bq = 32;
@@ -79,7 +83,7 @@ int head_group(int nheads, size_t bytes_per_head, size_t budget) {
 int build_problem(const fa_params* p, const Tiles& t, Problem* pr) {
   if (!p) return FA_ERR_NULL;
   if (p->abi_version != FA_ABI_VERSION) return FA_ERR_VERSION;
-  if (p->dtype != FA_DTYPE_BF16 && p->dtype != FA_DTYPE_F32) return FA_ERR_DTYPE;
+  if (p->dtype != FA_DTYPE_BF16 && p->dtype != FA_DTYPE_F32 && p->dtype != FA_DTYPE_FP8_E4M3) return FA_ERR_DTYPE;
   if (p->B < 1 || p->Hq < 1 || p->Hkv < 1 || p->Sq < 1 || p->Skv < 1) return FA_ERR_SHAPE;
   if (p->Hq % p->Hkv != 0) return FA_ERR_SHAPE;
   if (p->D != 32 && p->D != 64 && p->D != 128) return FA_ERR_UNSUPPORTED;
@@ -108,7 +112,7 @@ int build_problem(const fa_params* p, const Tiles& t, Problem* pr) {
   // heads per level-major group: as many as keep their K/V (forward, dQ) or
   // Q/dO (dK/dV, all q heads of a kv head) within the group budget
   {
-    const size_t es = p->dtype == FA_DTYPE_BF16 ? 2 : 4;
+    const size_t es = p->dtype == FA_DTYPE_BF16 ? 2 : p->dtype == FA_DTYPE_F32 ? 4 : 1;
     const size_t kv_head = 2 * (size_t)p->Skv * p->D * es / (size_t)(p->Hq / p->Hkv);
     const size_t q_heads = 2 * (size_t)p->Sq * p->D * es * (size_t)(p->Hq / p->Hkv);
     r.head_group_q = head_group(p->B * p->Hq, kv_head, kGroupBytesQ);
@@ -189,6 +193,7 @@ int bwd_d(const BwdArgs& a, int D, const Tiles& t, int stages, hipStream_t s) {
 // Validates the params for the requested backward stages and launches them.
 int bwd_stages(const fa_params* p, BwdArgs& a, int stages, hipStream_t s) {
   if (!p) return FA_ERR_NULL;
+  if (p->dtype == FA_DTYPE_FP8_E4M3) return FA_ERR_DTYPE;  // the fp8 path is forward-only
   Tiles t;
   int rc = default_tiles(p, &t);
   if (rc) return rc;
@@ -308,6 +313,7 @@ size_t split_bytes(const fa_params* p, int n) {
 int fwd_launch(const fa_params* p, const fa_kv_cache* kv, const void* q, const void* k, const void* v, void* o,
                float* lse, bool split, int n_splits, void* workspace, size_t workspace_bytes, void* stream) {
   if (!p) return FA_ERR_NULL;
+  if (p->dtype == FA_DTYPE_FP8_E4M3) return FA_ERR_DTYPE;  // fa_fwd_fp8
   if (n_splits > 64) return FA_ERR_SHAPE;
   Tiles t;
   int rc = default_tiles(p, &t);
@@ -393,6 +399,56 @@ int fa_fwd(const fa_params* p, const void* q, const void* k, const void* v, void
   return fwd_launch(p, nullptr, q, k, v, o, lse, false, 1, nullptr, 0, stream);
 }
 
+int fa_fwd_fp8(const fa_params* p, const fa_fp8_inputs* in, void* o, float* lse, void* stream) {
+  if (!p || !in) return FA_ERR_NULL;
+  if (p->dtype != FA_DTYPE_FP8_E4M3) return FA_ERR_DTYPE;
+  Tiles t;
+  int rc = default_tiles(p, &t);
+  if (rc) return rc;
+  fa::Fp8FwdArgs a;
+  rc = build_problem(p, t, &a.p);
+  if (rc) return rc;
+  if (p->D != 64 && p->D != 128) return FA_ERR_UNSUPPORTED;
+  if (!interval_masks(a.p)) return FA_ERR_UNSUPPORTED;  // document labels: contiguous runs only
+  if (!in->q || !in->k || !in->vt || !in->q_scale || !in->k_scale || !in->v_scale || !o || !lse) return FA_ERR_NULL;
+  if (!aligned16({in->q, in->k, in->vt, o})) return FA_ERR_SHAPE;
+  if (in->v_ld < p->Skv || in->v_ld % 128) return FA_ERR_SHAPE;
+  if ((long long)p->D * in->v_ld > 0xffffffffll || (long long)p->Skv * p->D > 0xffffffffll ||
+      (long long)p->Sq * p->D > 0xffffffffll)
+    return FA_ERR_SHAPE;  // one head's rows within a 32-bit buffer range
+  if (a.p.has_tables && (a.p.mblk_q % t.bm || a.p.mblk_kv % t.bn)) return FA_ERR_TABLES;
+  if (a.p.has_tables && !a.p.kv_num && !a.p.full_kv_num) return FA_ERR_TABLES;
+  a.q = static_cast<const uint8_t*>(in->q);
+  a.k = static_cast<const uint8_t*>(in->k);
+  a.vt = static_cast<const uint8_t*>(in->vt);
+  a.ldv = in->v_ld;
+  a.q_scale = in->q_scale;
+  a.k_scale = in->k_scale;
+  a.v_scale = in->v_scale;
+  a.o = o;
+  a.lse = lse;
+  return fa::launch_fwd_fp8(a, p->D, has_mods(a.p), static_cast<hipStream_t>(stream));
+}
+
+int fa_quantize_fp8(const void* x, int32_t heads, int32_t S, int32_t D, int32_t transpose, void* out, float* scale,
+                    void* stream) {
+  if (!x || !out || !scale) return FA_ERR_NULL;
+  if (heads < 1 || S < 1 || (transpose != 0 && transpose != 1)) return FA_ERR_SHAPE;
+  if (D != 32 && D != 64 && D != 128) return FA_ERR_UNSUPPORTED;
+  if (!aligned16({x, out})) return FA_ERR_SHAPE;
+  if ((long long)heads * cdiv(S, fa::kFp8ScaleRows) > 0x7fffffffll) return FA_ERR_SHAPE;
+  fa::QuantArgs a;
+  a.x = static_cast<const uint16_t*>(x);
+  a.out = static_cast<uint8_t*>(out);
+  a.scale = scale;
+  a.heads = heads;
+  a.S = S;
+  a.D = D;
+  a.ld = cdiv(S, fa::kFp8ScaleRows) * fa::kFp8ScaleRows;
+  a.transpose = transpose;
+  return fa::launch_quant_fp8(a, static_cast<hipStream_t>(stream));
+}
+
 size_t fa_fwd_kvcache_workspace_bytes(const fa_params* p, const fa_kv_cache* kv, int n_splits) {
   (void)kv;
   return fa_fwd_splitkv_workspace_bytes(p, n_splits);
@@ -436,6 +492,7 @@ size_t fa_bwd_noalloc_max_rows(void) { return kScratchFloats; }
 int fa_bwd_noalloc(const fa_params* p, const void* q, const void* k, const void* v, const void* o,
                    const float* lse, const void* dout, void* dq, void* dk, void* dv, void* stream) {
   if (!p) return FA_ERR_NULL;
+  if (p->dtype == FA_DTYPE_FP8_E4M3) return FA_ERR_DTYPE;  // the fp8 path is forward-only
   if (!q || !k || !v || !o || !lse || !dout || !dq || !dk || !dv) return FA_ERR_NULL;
   if (!aligned16({q, k, v, o, dout, dq, dk, dv})) return FA_ERR_SHAPE;
   if (p->B < 1 || p->Hq < 1 || p->Sq < 1) return FA_ERR_SHAPE;

@@ -8,6 +8,7 @@
 #include "../../include/flexattn.h"
 #include "bwd.h"
 #include "fwd.h"
+#include "fwd_fp8.h"
 
 namespace fa {
 
@@ -41,5 +42,10 @@ template <typename T, int D, bool M>
 int launch_dkdv(const BwdArgs& a, const Tiles& t, hipStream_t s);
 template <typename T, int D>
 int launch_delta(const BwdArgs& a, hipStream_t s);  // Delta = rowsum(dO * O)
+
+// fp8 forward (D = 64 or 128, 128 x 64 tiles) and the bf16 -> e4m3 block
+// quantiser (kernels_fp8.hip)
+int launch_fwd_fp8(const Fp8FwdArgs& a, int D, bool mods, hipStream_t s);
+int launch_quant_fp8(const QuantArgs& a, hipStream_t s);
 
 }  // namespace fa

@@ -38,6 +38,7 @@ from pallas_flexattn.block_mask import (
     create_causal_block_mask,
     create_sliding_window_block_mask,
 )
+from pallas_flexattn.fp8 import Fp8Tensor, dequantize_fp8, flex_attention_fp8, quantize_fp8
 from pallas_flexattn.kernel_tuner import (
     get_optimal_params,
     get_kernel_config,
@@ -66,6 +67,10 @@ __all__ = [
     "flex_decode",
     "flex_attention_varlen",
     "varlen_mask",
+    "flex_attention_fp8",
+    "quantize_fp8",
+    "dequantize_fp8",
+    "Fp8Tensor",
     "flash_attention_bwd_preprocess",
     "flash_attention_bwd_dkv",
     "flash_attention_bwd_dq",

@@ -14,6 +14,7 @@ ABI_VERSION = 2
 
 DTYPE_BF16 = 0
 DTYPE_F32 = 1
+DTYPE_FP8_E4M3 = 2
 
 _i32 = ctypes.c_int32
 _pi32 = ctypes.c_void_p
@@ -64,7 +65,13 @@ class FaKvCache(ctypes.Structure):
                 ("kv_lens", _pi32)]
 
 
-EXPORTED = ("fa_fwd", "fa_fwd_splitkv", "fa_fwd_splitkv_workspace_bytes", "fa_fwd_kvcache",
+class FaFp8Inputs(ctypes.Structure):
+    """Mirror of ``struct fa_fp8_inputs`` (include/flexattn.h)."""
+    _fields_ = [("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("vt", ctypes.c_void_p), ("v_ld", _i32),
+                ("q_scale", _pf), ("k_scale", _pf), ("v_scale", _pf)]
+
+
+EXPORTED = ("fa_fwd", "fa_fwd_fp8", "fa_quantize_fp8", "fa_fwd_splitkv", "fa_fwd_splitkv_workspace_bytes", "fa_fwd_kvcache",
             "fa_fwd_kvcache_workspace_bytes", "fa_bwd", "fa_bwd_workspace_bytes",
             "fa_bwd_noalloc", "fa_bwd_noalloc_max_rows", "fa_bwd_preprocess", "fa_bwd_dkdv", "fa_bwd_dq",
             "fa_mask_build_workspace_bytes", "fa_build_block_mask", "fa_strerror", "fa_abi_version",
@@ -101,6 +108,11 @@ def load():
     KV = ctypes.POINTER(FaKvCache)
     lib.fa_fwd_kvcache.argtypes = [P, KV, v, v, v, v, v, ctypes.c_int, v, ctypes.c_size_t, v]
     lib.fa_fwd_kvcache.restype = ctypes.c_int
+    lib.fa_fwd_fp8.argtypes = [P, ctypes.POINTER(FaFp8Inputs), v, v, v]
+    lib.fa_fwd_fp8.restype = ctypes.c_int
+    i32 = ctypes.c_int32
+    lib.fa_quantize_fp8.argtypes = [v, i32, i32, i32, i32, v, v, v]
+    lib.fa_quantize_fp8.restype = ctypes.c_int
     lib.fa_fwd_kvcache_workspace_bytes.argtypes = [P, KV, ctypes.c_int]
     lib.fa_fwd_kvcache_workspace_bytes.restype = ctypes.c_size_t
     lib.fa_bwd.argtypes = [P, v, v, v, v, v, v, v, v, v, v, ctypes.c_size_t, v]

@@ -51,6 +51,8 @@ def _dtype_code(t):
         return _lib.DTYPE_BF16, "bf16"
     if t.dtype == torch.float32:
         return _lib.DTYPE_F32, "fp32"
+    if t.dtype == torch.float8_e4m3fn:
+        return _lib.DTYPE_FP8_E4M3, "fp8"
     raise TypeError(f"unsupported dtype {t.dtype}: the MI355X kernels take bfloat16 or float32")
 
 

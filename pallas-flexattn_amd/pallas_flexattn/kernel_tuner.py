@@ -129,7 +129,7 @@ def print_kernel_config(
 SUPPORTED_BLOCK_M = (64, 128, 256)
 SUPPORTED_BLOCK_N = {"bf16": (32, 64, 128), "fp32": (32,)}
 SUPPORTED_BLOCK_KV = {"bf16": (64, 128), "fp32": (128,)}
-DEFAULT_TILES = {"bf16": (128, 64, 128), "fp32": (128, 32, 128)}
+DEFAULT_TILES = {"bf16": (128, 64, 128), "fp32": (128, 32, 128), "fp8": (128, 64, 128)}
 
 
 def candidate_tiles(dtype: str, head_dim: int) -> Tuple[Tuple[int, int, int], ...]:

@@ -68,7 +68,8 @@ def _params(**kw):
 
 @pytest.mark.parametrize("kw,code", [
     (dict(abi_version=99), -8), (dict(dtype=7), -3), (dict(D=48), -4), (dict(Hq=3, Hkv=2), -2),
-    (dict(Sq=0), -2), (dict(block_m=96), -4), (dict(softcap=-1.0), -2),
+    (dict(Sq=0), -2), (dict(block_m=96), -4), (dict(softcap=-1.0), -2), (dict(dtype=2), -3),
+    (dict(block_n=128, D=32), -4), (dict(block_kv=64, D=32), -4), (dict(block_m=256, D=32), -4),
     (dict(q_doc_ids=1234), -1),
     (dict(kv_num_blocks=8, kv_indices=8, mask_block_q=0, mask_block_kv=128), -5),
     (dict(kv_num_blocks=8, kv_indices=8, mask_block_q=128, mask_block_kv=128, table_b=3, table_h=1), -5),
@@ -99,6 +100,30 @@ def test_null_pointers_and_small_workspace_rejected():
     assert need >= 2 * 128 * 4
     assert lib.fa_bwd(ctypes.byref(p), d, d, d, d, d, d, d, d, d, d, need - 1, None) == -6
     assert lib.fa_bwd_dq(ctypes.byref(p), d, d, d, d, d, None, d, None) == -1
+
+
+def test_fp8_entry_points_validate_before_any_launch():
+    lib = _lib.load()
+    d = 16
+    p = _params(dtype=_lib.DTYPE_FP8_E4M3)
+    inp = _lib.FaFp8Inputs(d, d, d, 128, d, d, d)
+    fwd = lambda p, inp: lib.fa_fwd_fp8(ctypes.byref(p), ctypes.byref(inp), d, d, None)  # noqa: E731
+    assert fwd(_params(), inp) == -3                      # bf16 params
+    assert fwd(_params(dtype=2, D=32), inp) == -4         # head dim 32
+    assert fwd(_params(dtype=2, block_n=32), inp) == -4   # tiles other than 128 x 64
+    assert fwd(p, _lib.FaFp8Inputs(d, d, d, 100, d, d, d)) == -2   # v_ld not a multiple of 128
+    assert fwd(p, _lib.FaFp8Inputs(d, d, d, 0, d, d, d)) == -2     # v_ld < Skv
+    assert fwd(p, _lib.FaFp8Inputs(d, d, None, 128, d, d, d)) == -1
+    assert fwd(p, _lib.FaFp8Inputs(d, d, d, 128, d, None, d)) == -1
+    # the bf16 / fp32 entry points refuse the fp8 dtype
+    assert lib.fa_bwd_dq(ctypes.byref(p), d, d, d, d, d, d, d, None) == -3
+    assert lib.fa_bwd_noalloc(ctypes.byref(p), d, d, d, d, d, d, d, d, d, None) == -3
+    # quantiser
+    assert lib.fa_quantize_fp8(d, 1, 128, 48, 0, d, d, None) == -4
+    assert lib.fa_quantize_fp8(d, 0, 128, 64, 0, d, d, None) == -2
+    assert lib.fa_quantize_fp8(d, 1, 128, 64, 2, d, d, None) == -2
+    assert lib.fa_quantize_fp8(None, 1, 128, 64, 0, d, d, None) == -1
+    assert lib.fa_quantize_fp8(24, 1, 128, 64, 0, d, d, None) == -2  # misaligned
 
 
 def _mask_build(**kw):
