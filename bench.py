@@ -36,6 +36,7 @@ import numpy as np  # noqa: E402
 
 METRIC = "effective TFLOP/s fwd and fwd+bwd (unmasked FLOPs), % of bf16 MFMA peak"
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA: 256 CU x 4 SIMD x 1024 FLOP/clk x 2.4 GHz ("2.5 PFLOP/s")
+PEAK_FP8_TFLOPS = 5033.2   # dense fp8 MFMA, twice the bf16 rate ("5.0 PFLOP/s")
 
 
 def log(msg):
@@ -387,6 +388,30 @@ def main():
     log(f"flex_attention fwd+bwd: {api_ms:.3f} ms/step (Runner {ms_step:.3f})")
     del qq, kk, vv
 
+    # the fp8 forward on the same workload: q, k, v quantised once (timed
+    # apart), then the fp8 kernel alone, inputs resident in HBM
+    fp8 = None
+    if D in (64, 128):
+        from pallas_flexattn.fp8 import Fp8Runner, quantize_fp8
+
+        def quant():
+            return quantize_fp8(tq), quantize_fp8(tk), quantize_fp8(tv, transpose=True)
+
+        q8, k8, v8 = quant()
+        warm(quant, min_s=0.1)
+        quant_ms = time_region(quant, args.steps, stream)
+        fr = Fp8Runner(q8, k8, v8, score_mod=cfg["score"], block_mask=bmask, enable_gqa=Hq != Hkv)
+        warm(fr.fwd, min_s=0.2)
+        fp8_ms = time_region(fr.fwd, args.steps, stream)
+        fp8_tflops = flop_fwd / (fp8_ms * 1e-3) / 1e12
+        fp8 = {"workload": cfg["workload"].replace("fwd+bwd", "fwd").replace("bf16", "fp8 e4m3 (128-row block scales)"),
+               "ms": round(fp8_ms, 4), "tflops": round(fp8_tflops, 2),
+               "pct_fp8_peak": round(100 * fp8_tflops / PEAK_FP8_TFLOPS, 2), "peak_tflops": PEAK_FP8_TFLOPS,
+               "speedup_vs_bf16_fwd": round(ms_fwd / fp8_ms, 3), "quantize_qkv_ms": round(quant_ms, 4)}
+        log(f"fp8 forward: {fp8_ms:.3f} ms ({fp8_tflops:.1f} TFLOP/s, {ms_fwd / fp8_ms:.2f}x bf16); "
+            f"quantise q, k, v {quant_ms:.3f} ms")
+        del fr, q8, k8, v8
+
     sparsity = None
     if args.dense_ref:
         dense = Runner(tq, tk, tv, tdo, score_mod=cfg["score"])
@@ -451,6 +476,7 @@ def main():
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": measured_traffic(args.config, dom)},
         "cpu_baseline": cpu,
+        "fp8_forward": fp8,
         "other_configs": others,
     }
     if sparsity is not None:

@@ -74,8 +74,45 @@ def flex_attention_fp8(query, key, value, score_mod=None, block_mask: Optional[B
     or a transposed :class:`Fp8Tensor`.  Masks, block tables and score mods
     as :func:`flex_attention` (built-in descriptors; document labels as
     contiguous runs).  Returns bf16 O (and float32 LSE)."""
+    r = Fp8Runner(query, key, value, score_mod, block_mask, scale, enable_gqa)
+    r.fwd()
+    return (r.o, r.lse) if return_lse else r.o
+
+
+class Fp8Runner:
+    """One fp8 forward problem bound to its inputs and outputs: the plan,
+    the fa_fp8_inputs struct and O / LSE are built once; ``fwd()`` only
+    enqueues the kernel on the current stream (as ``flash_attn.Runner`` does
+    for the bf16 path; used by the benchmark)."""
+
+    def __init__(self, query, key, value, score_mod=None, block_mask: Optional[BlockMask] = None,
+                 scale: Optional[float] = None, enable_gqa: bool = False):
+        import torch
+        from .flash_attn import _get_plan, _resolve, _ShapeOnly, _tables_for
+        q8, k8, v8, mask, score, dims = _prepare(query, key, value, score_mod, block_mask, enable_gqa, _resolve)
+        B, Hq, Sq, D, Hkv, Skv = dims
+        dev = q8.data.device
+        f8 = torch.float8_e4m3fn
+        qs, ks = _ShapeOnly((B, Hq, Sq, D), dev, f8), _ShapeOnly((B, Hkv, Skv, D), dev, f8)
+        block_mask, tiles = _tables_for(mask, None, block_mask, qs, ks, DEFAULT_TILES["fp8"])
+        self.plan = _get_plan(qs, ks, mask, score, scale, block_mask, tiles)
+        self.inputs = (q8, k8, v8, block_mask)  # kept alive with the struct's pointers
+        self.o = torch.empty((B, Hq, Sq, D), device=dev, dtype=torch.bfloat16)
+        self.lse = torch.empty((B, Hq, Sq), device=dev, dtype=torch.float32)
+        self.args = _lib.FaFp8Inputs(q8.data.data_ptr(), k8.data.data_ptr(), v8.data.data_ptr(), v8.data.shape[3],
+                                     q8.scale.data_ptr(), k8.scale.data_ptr(), v8.scale.data_ptr())
+        self.lib = _lib.load()
+
+    def fwd(self):
+        import torch
+        _lib.check(self.lib.fa_fwd_fp8(self.plan.ptr(), _lib.ctypes.byref(self.args), self.o.data_ptr(),
+                                       self.lse.data_ptr(), torch.cuda.current_stream().cuda_stream))
+
+
+def _prepare(query, key, value, score_mod, block_mask, enable_gqa, resolve):
+    """Quantised inputs (bf16 tensors are quantised here), the resolved mask /
+    score descriptors and the dims (B, Hq, Sq, D, Hkv, Skv), validated."""
     import torch
-    from .flash_attn import _get_plan, _resolve, _ShapeOnly, _stream, _tables_for
     q8 = query if isinstance(query, Fp8Tensor) else quantize_fp8(query)
     k8 = key if isinstance(key, Fp8Tensor) else quantize_fp8(key)
     v8 = value if isinstance(value, Fp8Tensor) else quantize_fp8(value, transpose=True)
@@ -92,22 +129,10 @@ def flex_attention_fp8(query, key, value, score_mod=None, block_mask: Optional[B
     if D not in (64, 128):
         raise ValueError("the fp8 forward takes head dims 64 and 128")
     mask_mod = block_mask.mask_mod if block_mask is not None else None
-    mask, score, mods = _resolve(mask_mod, score_mod)
+    mask, score, mods = resolve(mask_mod, score_mod)
     if mods is not None:
         raise NotImplementedError("the fp8 forward takes the built-in mask / score descriptors")
-    dev = q8.data.device
-    f8 = torch.float8_e4m3fn
-    qs, ks = _ShapeOnly((B, Hq, Sq, D), dev, f8), _ShapeOnly((B, Hkv, Skv, D), dev, f8)
-    tiles = DEFAULT_TILES["fp8"]
-    block_mask, tiles = _tables_for(mask, None, block_mask, qs, ks, tiles)
-    plan = _get_plan(qs, ks, mask, score, scale, block_mask, tiles)
-    o = torch.empty((B, Hq, Sq, D), device=dev, dtype=torch.bfloat16)
-    lse = torch.empty((B, Hq, Sq), device=dev, dtype=torch.float32)
     for t in (q8, k8, v8):
         if not (t.data.is_contiguous() and t.scale.is_contiguous() and t.scale.dtype == torch.float32):
             raise ValueError("Fp8Tensor data and scales must be contiguous, scales float32")
-    inp = _lib.FaFp8Inputs(q8.data.data_ptr(), k8.data.data_ptr(), v8.data.data_ptr(), v8.data.shape[3],
-                           q8.scale.data_ptr(), k8.scale.data_ptr(), v8.scale.data_ptr())
-    lib = _lib.load()
-    _lib.check(lib.fa_fwd_fp8(plan.ptr(), _lib.ctypes.byref(inp), o.data_ptr(), lse.data_ptr(), _stream()))
-    return (o, lse) if return_lse else o
+    return q8, k8, v8, mask, score, (B, Hq, Sq, D, Hkv, Skv)
