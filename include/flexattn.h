@@ -180,6 +180,23 @@ int fa_fwd_fp8(const fa_params *p, const fa_fp8_inputs *in, void *o, float *lse,
 int fa_quantize_fp8(const void *x, int32_t heads, int32_t S, int32_t D, int32_t transpose, void *out, float *scale,
                     void *stream);
 
+/* Host twins of fa_fwd, fa_bwd_preprocess, fa_bwd_dkdv, fa_bwd_dq and fa_bwd:
+ * the same params and results on HOST memory, computed by C++ threads (all
+ * hardware threads for nthreads <= 0) -- the reference's interpret=True
+ * (its Pallas kernels run on the CPU, flash_attn.py:121,156,182,197,270,304,
+ * 373,401).  bf16 / fp32, any D up to 1024, window / document masks, ALiBi,
+ * soft-cap and block tables as the GPU path (tile fields ignored); fp32
+ * arithmetic with the GPU kernels' bf16 roundings.  No GPU is touched and
+ * the GPU entry points never call them. */
+int fa_fwd_host(const fa_params *p, const void *q, const void *k, const void *v, void *o, float *lse, int nthreads);
+int fa_bwd_preprocess_host(const fa_params *p, const void *o, const void *dout, float *delta, int nthreads);
+int fa_bwd_dkdv_host(const fa_params *p, const void *q, const void *k, const void *v, const void *dout,
+                     const float *lse, const float *delta, void *dk, void *dv, int nthreads);
+int fa_bwd_dq_host(const fa_params *p, const void *q, const void *k, const void *v, const void *dout,
+                   const float *lse, const float *delta, void *dq, int nthreads);
+int fa_bwd_host(const fa_params *p, const void *q, const void *k, const void *v, const void *o, const float *lse,
+                const void *dout, void *dq, void *dk, void *dv, int nthreads);
+
 /* Bytes of device scratch fa_bwd needs for these params. */
 size_t fa_bwd_workspace_bytes(const fa_params *p);
 

@@ -71,7 +71,8 @@ class FaFp8Inputs(ctypes.Structure):
                 ("q_scale", _pf), ("k_scale", _pf), ("v_scale", _pf)]
 
 
-EXPORTED = ("fa_fwd", "fa_fwd_fp8", "fa_quantize_fp8", "fa_fwd_splitkv", "fa_fwd_splitkv_workspace_bytes", "fa_fwd_kvcache",
+EXPORTED = ("fa_fwd", "fa_fwd_fp8", "fa_quantize_fp8", "fa_fwd_host", "fa_bwd_preprocess_host", "fa_bwd_dkdv_host",
+            "fa_bwd_dq_host", "fa_bwd_host", "fa_fwd_splitkv", "fa_fwd_splitkv_workspace_bytes", "fa_fwd_kvcache",
             "fa_fwd_kvcache_workspace_bytes", "fa_bwd", "fa_bwd_workspace_bytes",
             "fa_bwd_noalloc", "fa_bwd_noalloc_max_rows", "fa_bwd_preprocess", "fa_bwd_dkdv", "fa_bwd_dq",
             "fa_mask_build_workspace_bytes", "fa_build_block_mask", "fa_strerror", "fa_abi_version",
@@ -108,6 +109,14 @@ def load():
     KV = ctypes.POINTER(FaKvCache)
     lib.fa_fwd_kvcache.argtypes = [P, KV, v, v, v, v, v, ctypes.c_int, v, ctypes.c_size_t, v]
     lib.fa_fwd_kvcache.restype = ctypes.c_int
+    ci = ctypes.c_int
+    lib.fa_fwd_host.argtypes = [P, v, v, v, v, v, ci]
+    lib.fa_bwd_preprocess_host.argtypes = [P, v, v, v, ci]
+    lib.fa_bwd_dkdv_host.argtypes = [P, v, v, v, v, v, v, v, v, ci]
+    lib.fa_bwd_dq_host.argtypes = [P, v, v, v, v, v, v, v, ci]
+    lib.fa_bwd_host.argtypes = [P, v, v, v, v, v, v, v, v, v, ci]
+    for n in ("fa_fwd_host", "fa_bwd_preprocess_host", "fa_bwd_dkdv_host", "fa_bwd_dq_host", "fa_bwd_host"):
+        getattr(lib, n).restype = ci
     lib.fa_fwd_fp8.argtypes = [P, ctypes.POINTER(FaFp8Inputs), v, v, v]
     lib.fa_fwd_fp8.restype = ctypes.c_int
     i32 = ctypes.c_int32

@@ -56,19 +56,24 @@ def _dtype_code(t):
     raise TypeError(f"unsupported dtype {t.dtype}: the MI355X kernels take bfloat16 or float32")
 
 
-def _check_interpret(interpret):
-    if interpret:
-        raise NotImplementedError(
-            "interpret=True ran the Pallas interpreter on the host; this MI355X build only executes its "
-            "HIP kernels on the GPU. Pass GPU tensors with interpret=False (mha_reference gives a "
-            "materialised reference result).")
+def _check_interpret(interpret, t):
+    """Whether a call runs on the host: interpret=True (the reference's Pallas
+    interpreter on the CPU) runs the library's host twins (fa_*_host) on CPU
+    tensors; the GPU path takes GPU tensors only (no fallback either way)."""
+    if interpret and t.is_cuda:
+        raise ValueError("interpret=True executes on the host: pass CPU tensors (GPU tensors run with "
+                         "interpret=False)")
+    return bool(interpret)
 
 
-def _check_inputs(q, k, v):
+def _check_inputs(q, k, v, host=False):
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError("q, k, v must be (B, H, T, D)")
-    if not (q.is_cuda and k.is_cuda and v.is_cuda):
-        raise ValueError("q, k, v must be GPU tensors")
+    if host:
+        if q.is_cuda or k.is_cuda or v.is_cuda:
+            raise ValueError("the host path (interpret=True) takes CPU tensors")
+    elif not (q.is_cuda and k.is_cuda and v.is_cuda):
+        raise ValueError("q, k, v must be GPU tensors (CPU tensors run with interpret=True)")
     if q.dtype != k.dtype or q.dtype != v.dtype:
         raise TypeError("q, k, v must share a dtype")
     B, Hq, Sq, D = q.shape
@@ -354,10 +359,19 @@ def _dense16(t):
     return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
-def _fwd_core(q, k, v, mask, score, scale, block_mask, tiles, mods=None):
-    """Forward through fa_fwd (fa_mods_fwd with user mods) -> (o, lse fp32, plan)."""
+def _host_mods(mods):
+    if mods is not None:
+        raise NotImplementedError("interpret=True runs the built-in mask / score descriptors on the host; "
+                                  "traced callables run on the GPU (interpret=False)")
+
+
+def _fwd_core(q, k, v, mask, score, scale, block_mask, tiles, mods=None, host=False):
+    """Forward through fa_fwd (fa_mods_fwd with user mods; fa_fwd_host on the
+    host path) -> (o, lse fp32, plan)."""
     torch = _torch()
-    _check_inputs(q, k, v)
+    _check_inputs(q, k, v, host)
+    if host:
+        _host_mods(mods)
     q, k, v = _dense16(q), _dense16(k), _dense16(v)
     if mods is not None:
         tiles = _MODS_TILES[_dtype_code(q)[1]]
@@ -367,7 +381,9 @@ def _fwd_core(q, k, v, mask, score, scale, block_mask, tiles, mods=None):
     lse = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
     lib = _lib.load()
     ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr())
-    if mods is None:
+    if host:
+        _lib.check(lib.fa_fwd_host(plan.ptr(), *ptrs, 0))
+    elif mods is None:
         _lib.check(lib.fa_fwd(plan.ptr(), *ptrs, _stream()))
     else:
         h, bufs, n = _mods_args(mods, plan, q, score)
@@ -375,12 +391,14 @@ def _fwd_core(q, k, v, mask, score, scale, block_mask, tiles, mods=None):
     return o, lse, plan
 
 
-def _bwd_core(q, k, v, o, lse, do, mask, score, scale, block_mask, tiles, mods=None, plan=None):
-    """Backward through fa_bwd (fa_mods_bwd with user mods) -> (dq, dk, dv).
-    ``plan`` is the forward's plan when the caller has it (same problem),
-    else one is looked up."""
+def _bwd_core(q, k, v, o, lse, do, mask, score, scale, block_mask, tiles, mods=None, host=False, plan=None):
+    """Backward through fa_bwd (fa_mods_bwd with user mods; fa_bwd_host on
+    the host path) -> (dq, dk, dv).  ``plan`` is the forward's plan when the
+    caller has it (same problem), else one is looked up."""
     torch = _torch()
-    _check_inputs(q, k, v)
+    _check_inputs(q, k, v, host)
+    if host:
+        _host_mods(mods)
     if do.dtype != q.dtype:
         do = do.to(q.dtype)
     q, k, v, o, do = (_dense16(t) for t in (q, k, v, o, do))
@@ -394,6 +412,11 @@ def _bwd_core(q, k, v, o, lse, do, mask, score, scale, block_mask, tiles, mods=N
         block_mask, tiles = _tables_for(mask, mods, block_mask, q, k, tiles)
         plan = _get_plan(q, k, mask, score, scale, block_mask, tiles)
     lib = _lib.load()
+    if host:
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        _lib.check(lib.fa_bwd_host(plan.ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                   lse.data_ptr(), do.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), 0))
+        return dq, dk, dv
     ws_bytes = lib.fa_bwd_workspace_bytes(plan.ptr())
     ws = torch.empty(max(ws_bytes, 256), device=q.device, dtype=torch.uint8)
     dq = torch.empty_like(q)
@@ -443,22 +466,26 @@ def flash_attention_bwd_preprocess(o_flat, do_flat, block_r: int = DEFAULT_BLOCK
                                    interpret: bool = False):
     """Delta = rowsum(O * dO) (``flash_attn.py:168-203``), shape o.shape[:-1].
     Returned in fp32 (the reference stores it in O's dtype)."""
-    _check_interpret(interpret)
+    host = _check_interpret(interpret, o_flat)
     torch = _torch()
     o4, do4 = _dense16(_as4d(o_flat)), _dense16(_as4d(do_flat).to(o_flat.dtype))
     plan, _ = _stage_plan(o4, o4, None, block_r, DEFAULT_BLOCK_C)
     delta = torch.empty(o4.shape[:3], device=o4.device, dtype=torch.float32)
-    _lib.check(_lib.load().fa_bwd_preprocess(plan.ptr(), o4.data_ptr(), do4.data_ptr(), delta.data_ptr(),
-                                             _stream()))
+    if host:
+        _lib.check(_lib.load().fa_bwd_preprocess_host(plan.ptr(), o4.data_ptr(), do4.data_ptr(),
+                                                      delta.data_ptr(), 0))
+    else:
+        _lib.check(_lib.load().fa_bwd_preprocess(plan.ptr(), o4.data_ptr(), do4.data_ptr(), delta.data_ptr(),
+                                                 _stream()))
     return delta.reshape(o_flat.shape[:-1])
 
 
-def _stage_inputs(q_flat, k_flat, v_flat, do_flat, logsumexp_flat, d_flat, qk_scale, softmax_scale):
+def _stage_inputs(q_flat, k_flat, v_flat, do_flat, logsumexp_flat, d_flat, qk_scale, softmax_scale, host=False):
     torch = _torch()
     if abs(qk_scale - softmax_scale) > 1e-12 * max(abs(qk_scale), 1.0):
         raise NotImplementedError("the kernels apply one softmax scale to both S and dS")
     q4, k4, v4 = (_dense16(_as4d(t)) for t in (q_flat, k_flat, v_flat))
-    _check_inputs(q4, k4, v4)
+    _check_inputs(q4, k4, v4, host)
     do4 = _dense16(_as4d(do_flat).to(q4.dtype))
     lse = logsumexp_flat.to(torch.float32).reshape(q4.shape[:3]).contiguous()
     delta = d_flat.to(torch.float32).reshape(q4.shape[:3]).contiguous()
@@ -470,15 +497,18 @@ def flash_attention_bwd_dkv(q_flat, k_flat, v_flat, do_flat, logsumexp_flat, d_f
                             num_warps: int = DEFAULT_NUM_WARPS, num_stages: int = DEFAULT_NUM_STAGES,
                             mask_mod: Optional[MaskMod] = None, interpret: bool = False):
     """dK, dV (``flash_attn.py:206-310``) from q, k, v, dO, LSE and Delta."""
-    _check_interpret(interpret)
+    host = _check_interpret(interpret, q_flat)
     torch = _torch()
     q4, k4, v4, do4, lse, delta = _stage_inputs(q_flat, k_flat, v_flat, do_flat, logsumexp_flat, d_flat,
-                                                qk_scale, softmax_scale)
+                                                qk_scale, softmax_scale, host)
     plan, mods = _stage_plan(q4, k4, mask_mod, block_r, block_c, qk_scale)
     dk, dv = torch.empty_like(k4), torch.empty_like(v4)
     ptrs = (q4.data_ptr(), k4.data_ptr(), v4.data_ptr(), do4.data_ptr(), lse.data_ptr(), delta.data_ptr(),
             dk.data_ptr(), dv.data_ptr())
-    if mods is None:
+    if host:
+        _host_mods(mods)
+        _lib.check(_lib.load().fa_bwd_dkdv_host(plan.ptr(), *ptrs, 0))
+    elif mods is None:
         _lib.check(_lib.load().fa_bwd_dkdv(plan.ptr(), *ptrs, _stream()))
     else:
         h, bufs, n = _mods_args(mods, plan, q4, None)
@@ -491,15 +521,18 @@ def flash_attention_bwd_dq(q_flat, k_flat, v_flat, do_flat, logsumexp_flat, d_fl
                            num_warps: int = DEFAULT_NUM_WARPS, num_stages: int = DEFAULT_NUM_STAGES,
                            mask_mod: Optional[MaskMod] = None, interpret: bool = False):
     """dQ (``flash_attn.py:313-407``) from q, k, v, dO, LSE and Delta."""
-    _check_interpret(interpret)
+    host = _check_interpret(interpret, q_flat)
     torch = _torch()
     q4, k4, v4, do4, lse, delta = _stage_inputs(q_flat, k_flat, v_flat, do_flat, logsumexp_flat, d_flat,
-                                                qk_scale, softmax_scale)
+                                                qk_scale, softmax_scale, host)
     plan, mods = _stage_plan(q4, k4, mask_mod, block_r, block_c, qk_scale)
     dq = torch.empty_like(q4)
     ptrs = (q4.data_ptr(), k4.data_ptr(), v4.data_ptr(), do4.data_ptr(), lse.data_ptr(), delta.data_ptr(),
             dq.data_ptr())
-    if mods is None:
+    if host:
+        _host_mods(mods)
+        _lib.check(_lib.load().fa_bwd_dq_host(plan.ptr(), *ptrs, 0))
+    elif mods is None:
         _lib.check(_lib.load().fa_bwd_dq(plan.ptr(), *ptrs, _stream()))
     else:
         h, bufs, n = _mods_args(mods, plan, q4, None)
@@ -586,9 +619,10 @@ def flash_attention_fwd(q, k, v, mask_mod: Optional[MaskMod] = None, block_r: in
                         block_c: int = DEFAULT_BLOCK_C, num_warps: int = DEFAULT_NUM_WARPS,
                         num_stages: int = DEFAULT_NUM_STAGES, interpret: bool = False):
     """Forward pass -> (o, logsumexp) with logsumexp in q's dtype (``flash_attn.py:111-165``)."""
-    _check_interpret(interpret)
+    host = _check_interpret(interpret, q)
     mask, _, mods = _resolve(mask_mod, None)
-    o, lse, _ = _fwd_core(q, k, v, mask, None, None, None, _ref_tiles(q, block_r, block_c, _sparse(mask)), mods)
+    o, lse, _ = _fwd_core(q, k, v, mask, None, None, None, _ref_tiles(q, block_r, block_c, _sparse(mask)), mods,
+                          host)
     return o, lse.to(q.dtype)
 
 
@@ -598,10 +632,10 @@ def flash_attention_bwd(q, k, v, o, logsumexp, do, mask_mod: Optional[MaskMod] =
                         interpret: bool = False):
     """Backward pass -> (dq, dk, dv) (``flash_attn.py:410-461``).  ``logsumexp``
     may be in q's dtype (as returned by :func:`flash_attention_fwd`) or fp32."""
-    _check_interpret(interpret)
+    host = _check_interpret(interpret, q)
     mask, _, mods = _resolve(mask_mod, None)
     return _bwd_core(q, k, v, o, logsumexp, do, mask, None, None, None,
-                     _ref_tiles(q, block_r, block_c, _sparse(mask)), mods)
+                     _ref_tiles(q, block_r, block_c, _sparse(mask)), mods, host)
 
 
 class _FlexFn:
@@ -617,7 +651,8 @@ class _FlexFn:
             class FlexAttnFunction(torch.autograd.Function):
                 @staticmethod
                 def forward(ctx, q, k, v, cfg):
-                    o, lse, plan = _fwd_core(q, k, v, *cfg)  # cfg: mask, score, scale, block mask, tiles, mods
+                    # cfg: mask, score, scale, block mask, tiles, mods, host
+                    o, lse, plan = _fwd_core(q, k, v, *cfg)
                     ctx.save_for_backward(q, k, v, o, lse)
                     ctx.cfg = cfg
                     ctx.plan = plan
@@ -638,9 +673,9 @@ def flash_attention(q, k, v, mask_mod: Optional[MaskMod] = None, block_r: int = 
                     block_c: int = DEFAULT_BLOCK_C, num_warps: int = DEFAULT_NUM_WARPS,
                     num_stages: int = DEFAULT_NUM_STAGES, interpret: bool = False):
     """Flash attention with a custom backward (``flash_attn.py:464-504``)."""
-    _check_interpret(interpret)
+    host = _check_interpret(interpret, q)
     mask, _, mods = _resolve(mask_mod, None)
-    cfg = (mask, None, None, None, _ref_tiles(q, block_r, block_c, _sparse(mask)), mods)
+    cfg = (mask, None, None, None, _ref_tiles(q, block_r, block_c, _sparse(mask)), mods, host)
     o, _ = _FlexFn.get().apply(q, k, v, cfg)
     return o
 
@@ -816,6 +851,6 @@ def flex_attention(query, key, value, score_mod: Optional[ScoreSpec] = None,
     tiles = tuned_tiles(query.shape[2], query.shape[3], dname, block_mask is not None) or DEFAULT_TILES[dname]
     if any(o in opts for o in ("BLOCK_M", "BLOCK_N", "BLOCK_KV")):
         tiles = tuple(int(opts.get(o, d)) for o, d in zip(("BLOCK_M", "BLOCK_N", "BLOCK_KV"), DEFAULT_TILES[dname]))
-    cfg = (mask, score, scale, block_mask, tiles, mods)
+    cfg = (mask, score, scale, block_mask, tiles, mods, False)
     o, lse = _FlexFn.get().apply(query, key, value, cfg)
     return (o, lse) if return_lse else o

@@ -80,11 +80,9 @@ def test_score_spec_matches_formula():
         pf.compose_score_mods(pf.softcap_score_mod(5.0), pf.alibi_score_mod(4))
 
 
-def test_interpret_mode_and_untraceable_callables_raise():
+def test_untraceable_callables_raise():
     torch = pytest.importorskip("torch")
     x = torch.zeros(1, 1, 8, 32)
-    with pytest.raises(NotImplementedError):
-        pf.flash_attention(x, x, x, interpret=True)
     from pallas_flexattn.flash_attn import _resolve
     # callables are traced and lowered; Python control flow on traced indices cannot be
     with pytest.raises(NotImplementedError, match="control flow"):
