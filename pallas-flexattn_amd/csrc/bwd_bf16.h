@@ -27,7 +27,7 @@
 #include "dma.h"
 
 #ifndef FA_DKDV_APF
-#define FA_DKDV_APF 2
+#define FA_DKDV_APF 3  // measured: 2 -> 3 about 0.5 % faster at S = 8192, 4 no better
 #endif
 
 namespace fa {
