@@ -177,7 +177,8 @@ __device__ __forceinline__ void mfma_drain(f32x16& acc) {
 
 // Store of a wave's 32-row accumulator block as bf16 rows of a row-major
 // (rows, D) tensor.  In the MFMA 32x32 layout lane l holds row (l & 31) and
-// element e of tile i holds column 32 i + acc_row(e, l >> 5): stored directly,
+// element e of tile i holds column 32 i + 8 (e / 4) + 4 (l / 32) + e % 4 (the
+// A operand's rows in natural order, as transposing reads give them): stored directly,
 // every instruction would write 8 bytes into each of 32 rows.  The block is
 // staged instead through `stage` (the wave's own 32 * 2D bytes of LDS, 16-byte
 // chunks swizzled by the row) and written back 16 bytes per lane with
