@@ -110,9 +110,13 @@ struct TileDma {
 // acc += A(tileA rows 32j..) * bA[s]  and  acc2 += A(tileB rows 32j..) * bB[s]
 // over all k steps, operands fetched PF steps ahead (one step is two MFMAs,
 // 64 cycles; an LDS read under load takes longer than that).
-template <int D, int PF = 1>
+struct NoHook {
+  __device__ __forceinline__ void operator()(int) const {}
+};
+template <int D, int PF = 1, class Hook = NoHook>
 __device__ __forceinline__ void mma_rows2(const RowTile<D>& rt, const char* ta, const char* tb, int j,
-                                          const u32x4* ba, const u32x4* bb, f32x16& acc, f32x16& acc2) {
+                                          const u32x4* ba, const u32x4* bb, f32x16& acc, f32x16& acc2,
+                                          const Hook& hook = Hook()) {
   using E = Elt<uint16_t>;
   constexpr int KS = D / 16;
   constexpr int R = PF + 1;
@@ -130,6 +134,7 @@ __device__ __forceinline__ void mma_rows2(const RowTile<D>& rt, const char* ta, 
     }
     acc = E::mma(fa[s % R], ba[s], acc);
     acc2 = E::mma(fb[s % R], bb[s], acc2);
+    hook(s);
   }
 }
 
@@ -247,7 +252,7 @@ void dq_bf16_kernel(BwdArgs a) {
   // A single code path for full and partial tiles: only the in-place masking
   // of S^T is conditional, so the loop-carried accumulators keep their
   // registers.
-  auto tile = [&](int kbase, const char* kl, const char* vl, auto masked_c) {
+  auto tile = [&](int kbase, const char* kl, const char* vl, auto masked_c, auto&& copies) {
     constexpr bool kMasked = decltype(masked_c)::value;
     frag sf[2];
 #pragma unroll
@@ -255,7 +260,8 @@ void dq_bf16_kernel(BwdArgs a) {
       f32x16 sacc, pacc;
       zero(sacc);
       zero(pacc);
-      mma_rows2<D>(rt, kl, vl, j, qf, df, sacc, pacc);
+      if (j == 0) mma_rows2<D>(rt, kl, vl, j, qf, df, sacc, pacc, copies);
+      else mma_rows2<D>(rt, kl, vl, j, qf, df, sacc, pacc);
       float dsdx[16];
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
@@ -316,15 +322,37 @@ void dq_bf16_kernel(BwdArgs a) {
   __syncthreads();
   // (the buffer index stays a run-time value here: as a constant it costs
   // this 256-VGPR kernel spills)
+  // the next tile's copies are spread over the first sub-tile's k steps (as
+  // in the forward: issued back to back they queue at the texture unit;
+  // 0.7 % of this kernel at S = 8192, measured)
+  constexpr int IPW = TileDma<D, BN, NW>::IPW;
   auto step = [&](int it, auto masked_c) {
     const int buf = it & 1;
     const int kbase = kb_next;
-    if (it + 1 < n_it) {
+    const bool more = it + 1 < n_it;
+    i32x4 rk = {0, 0, 0, 0}, rv = {0, 0, 0, 0};
+    if (more) {
       kb_next = walk.kbase(ref_next);
-      issue(kb_next, buf ^ 1);
+      rk = TileDma<D, BN, NW>::rsrc(kbase_ptr, kb_next, P.Skv);
+      rv = TileDma<D, BN, NW>::rsrc(vbase_ptr, kb_next, P.Skv);
     }
+    char* nk = lds + (buf ^ 1) * TILE;
+    char* nv = lds + (2 + (buf ^ 1)) * TILE;
+    auto copies = [&](int s) {
+#pragma unroll
+      for (int i = 0; i < 2 * IPW; ++i)
+        if (i * KSTEPS / (2 * IPW) == s && more) {
+          if (i < IPW) dma.one(rk, i, nk, w);
+          else dma.one(rv, i - IPW, nv, w);
+        }
+    };
     if (it + 2 < n_it) ref_next = walk.fetch(it + 2);
-    if (kbase < P.Skv) tile(kbase, lds + buf * TILE, lds + (2 + buf) * TILE, masked_c);
+    if (kbase < P.Skv) {
+      tile(kbase, lds + buf * TILE, lds + (2 + buf) * TILE, masked_c, copies);
+    } else {
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) copies(s);
+    }
     wait_vmem();
     __syncthreads();
   };
