@@ -464,6 +464,8 @@ def main():
         "data": "synthetic (seeded normals rounded to bf16)",
         "config": {"workload": cfg["workload"], "B": B, "Hq": Hq, "Hkv": Hkv, "S": S, "D": D,
                    "mask_block": 128, "live_tiles": bmask.live_tiles(),
+                   "live_tiles_per_head": bmask.live_tiles() / (bmask.table_shape[0] * bmask.table_shape[1]),
+                   "reference_executed_tiles_per_head": ((S + 127) // 128) ** 2,
                    "unmasked_pairs_per_head": pairs / B},
         "fwdbwd_pct_peak": round(100 * fwdbwd_tflops / PEAK_BF16_TFLOPS, 2),
         "fwd_tflops": round(fwd_tflops, 2),
