@@ -39,8 +39,11 @@ namespace fa {
 // kCache: the KV-cache variant (GQA row packing, paged K / V, per-batch key
 // counts).  Kept out of the plain variant: its per-tile address logic costs
 // the training-shape forward 7 % even when unused (measured A/B).
+// Waves per SIMD: three for 32-key tiles (32 KiB of LDS; 168 registers, 8 %
+// faster than two at S = 8192, measured), two otherwise.
 template <int D, int BN, int NW, bool kMods, class Mod = BuiltinMod, bool kCache = false>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(occupancy_for(4 * BN * D * 2, NW, 2))))
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(
+    occupancy_for(4 * BN * D * 2, NW, BN == 32 ? 3 : 2))))
 void fwd_bf16_kernel(FwdArgs a) {
   using E = Elt<uint16_t>;
   using frag = E::frag;
@@ -271,19 +274,30 @@ void fwd_bf16_kernel(FwdArgs a) {
     l += rs;
   };
 
-  // Table entries are fetched two tiles ahead, resolved one tile ahead; the
-  // full tiles come first in the walk.
+  // The walk's kv-block indices come from one register: lane i holds entry
+  // e0 + i of the row (full list first), reloaded every 64 entries, so the
+  // tiles make no table loads (0.9 % at S = 8192, measured).
   // With split-KV this workgroup takes tiles [it0, it1) of the walk.
   const int n_full = walk.count_full();
   const int it0 = a.n_splits > 1 ? (int)((long long)n_it * split / a.n_splits) : 0;
   const int it1 = a.n_splits > 1 ? (int)((long long)n_it * (split + 1) / a.n_splits) : n_it;
-  int kb_next = 0;
-  TileRef ref_next{0, 0, 0};
-  if (it0 < it1) {
-    kb_next = walk.kbase(walk.fetch(it0));
-    issue(kb_next, 0);
-    if (it0 + 1 < it1) ref_next = walk.fetch(it0 + 1);
-  }
+  const int sub_log2 = log2_if_pow2(walk.sub);
+  int tab_e0 = -64, tab = 0;
+  auto tab_load = [&](int e0) {
+    const int e = e0 + lane;  // past a list's end the loads return 0 (never read)
+    const int vf = vload_i32(walk.full, e, walk.nfull);
+    const int vp = vload_i32(walk.part, e - walk.nfull, walk.npart);
+    tab = e < walk.nfull ? vf : vp;
+    tab_e0 = e0;
+  };
+  auto kbase_of = [&](int it) {  // first key of tile it (wave-uniform)
+    if (walk.dense) return it * BN;
+    const int bi = div_pow2_or(it, walk.sub, sub_log2);
+    if (bi - tab_e0 >= 64 || bi < tab_e0) tab_load(bi & ~63);
+    const int raw = __builtin_amdgcn_readlane(tab, bi - tab_e0);
+    return (raw < 0 || raw >= walk.nblk) ? kPastEnd : raw * walk.mblk + (it - bi * walk.sub) * BN;
+  };
+  if (it0 < it1) issue(kbase_of(it0), 0);
   // unconditional, so the wait-count analysis sees the register loads above
   // complete on every path into the loop
   wait_vmem();
@@ -293,15 +307,11 @@ void fwd_bf16_kernel(FwdArgs a) {
   // immediate offset (the loop below runs tiles in pairs).
   auto tile_step = [&](int it, auto buf_c) {
     constexpr int buf = decltype(buf_c)::value;
-    const int kbase = kb_next;
+    const int kbase = kbase_of(it);
     bool masked = it >= n_full;
     const bool more = it + 1 < it1;
     Copy nc;
-    if (more) {
-      kb_next = walk.kbase(ref_next);
-      nc = issue_plan(kb_next, buf ^ 1);
-    }
-    if (it + 2 < it1) ref_next = walk.fetch(it + 2);
+    if (more) nc = issue_plan(kbase_of(it + 1), buf ^ 1);
     if (kbase >= skv && more) {
 #pragma unroll
       for (int i = 0; i < 2 * IPW; ++i) issue_one(nc, i);
