@@ -96,6 +96,29 @@ struct KvWalk {
   }
 };
 
+// A kv walk's block indices held in one register: lane i holds entry e0 + i
+// of the row (full list first), reloaded every 64 entries, so the tiles make
+// no table loads (a load consumed by the walk would also wait for every copy
+// issued before it).
+struct KvTab {
+  int e0 = -64, reg = 0;
+  __device__ __forceinline__ void load(const KvWalk& w, int first, int lane) {
+    const int e = first + lane;  // past a list's end the loads return 0 (never read)
+    const int vf = vload_i32(w.full, e, w.nfull);
+    const int vp = vload_i32(w.part, e - w.nfull, w.npart);
+    reg = e < w.nfull ? vf : vp;
+    e0 = first;
+  }
+  // first key of tile it (wave-uniform)
+  __device__ __forceinline__ int kbase(const KvWalk& w, int it, int sub_log2, int lane) {
+    if (w.dense) return it * w.bn;
+    const int bi = div_pow2_or(it, w.sub, sub_log2);
+    if (bi - e0 >= 64 || bi < e0) load(w, bi & ~63, lane);
+    const int raw = __builtin_amdgcn_readlane(reg, bi - e0);
+    return (raw < 0 || raw >= w.nblk) ? kPastEnd : raw * w.mblk + (it - bi * w.sub) * w.bn;
+  }
+};
+
 template <typename T, int D, int BN, int NW, bool kMods, class Mod = BuiltinMod>
 __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdArgs a) {
   using E = Elt<T>;

@@ -274,29 +274,15 @@ void fwd_bf16_kernel(FwdArgs a) {
     l += rs;
   };
 
-  // The walk's kv-block indices come from one register: lane i holds entry
-  // e0 + i of the row (full list first), reloaded every 64 entries, so the
-  // tiles make no table loads (0.9 % at S = 8192, measured).
+  // The walk's block indices come from a register (KvTab: 0.9 % at S = 8192,
+  // measured against a table load per tile).
   // With split-KV this workgroup takes tiles [it0, it1) of the walk.
   const int n_full = walk.count_full();
   const int it0 = a.n_splits > 1 ? (int)((long long)n_it * split / a.n_splits) : 0;
   const int it1 = a.n_splits > 1 ? (int)((long long)n_it * (split + 1) / a.n_splits) : n_it;
   const int sub_log2 = log2_if_pow2(walk.sub);
-  int tab_e0 = -64, tab = 0;
-  auto tab_load = [&](int e0) {
-    const int e = e0 + lane;  // past a list's end the loads return 0 (never read)
-    const int vf = vload_i32(walk.full, e, walk.nfull);
-    const int vp = vload_i32(walk.part, e - walk.nfull, walk.npart);
-    tab = e < walk.nfull ? vf : vp;
-    tab_e0 = e0;
-  };
-  auto kbase_of = [&](int it) {  // first key of tile it (wave-uniform)
-    if (walk.dense) return it * BN;
-    const int bi = div_pow2_or(it, walk.sub, sub_log2);
-    if (bi - tab_e0 >= 64 || bi < tab_e0) tab_load(bi & ~63);
-    const int raw = __builtin_amdgcn_readlane(tab, bi - tab_e0);
-    return (raw < 0 || raw >= walk.nblk) ? kPastEnd : raw * walk.mblk + (it - bi * walk.sub) * BN;
-  };
+  KvTab tab;
+  auto kbase_of = [&](int it) { return tab.kbase(walk, it, sub_log2, lane); };
   if (it0 < it1) issue(kbase_of(it0), 0);
   // unconditional, so the wait-count analysis sees the register loads above
   // complete on every path into the loop
