@@ -24,11 +24,12 @@ int run_fwd(const FwdArgs& a, hipStream_t s) {
     if (interval_masks(a.p)) {  // bf16: LDS-DMA + transposing-read kernel
       const bool cache = a.pack > 1 || a.page_table || a.kv_lens;
       if constexpr (NW == 4 && BN == 64) {
-        // decode (every packed row in one 32-row block): one wave per
-        // workgroup and 32-key tiles, 4x less MFMA work on dead rows and half
-        // the LDS per workgroup; measured 5.72 against 5.40 TB/s of KV reads
-        // at B8 Hq32 Hkv8 Skv32768 (a plain streaming read reaches ~5.8)
-        if (cache && a.pack > 1 && a.pack * a.p.Sq <= 32 && D >= 64)
+        // split-KV decode (every packed row in one 32-row block): one wave
+        // per workgroup and 32-key tiles, 4x less MFMA work on dead rows and
+        // half the LDS per workgroup; measured 5.72 against 5.40 TB/s of KV
+        // reads at B8 Hq32 Hkv8 Skv32768 (a plain streaming read reaches
+        // ~5.8).  Unsplit, its grid of one-wave workgroups is too small.
+        if (cache && a.pack > 1 && a.pack * a.p.Sq <= 32 && a.n_splits > 1 && D >= 64)
           hipLaunchKernelGGL((fa::fwd_bf16_kernel<D, 32, 1, M, fa::BuiltinMod, true>), dim3(grid * a.n_splits),
                              dim3(64), 0, s, a);
         else if (cache)
