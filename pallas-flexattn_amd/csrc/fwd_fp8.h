@@ -185,18 +185,27 @@ void fwd_fp8_kernel(Fp8FwdArgs a) {
 
   // HBM -> LDS copies of the tile starting at key kb into buffer `buf`
   // (a tile past the end copies zeros: empty ranges at the head's base)
-  auto issue = [&](int kb, int buf) {
+  // (plan, then one copy instruction at a time: inside the walk they are
+  // spread over the S phase's MFMAs, as in the bf16 forward)
+  struct Copy { i32x4 rk, rv; char* kl; char* vl; };
+  auto issue_plan = [&](int kb, int buf) {
     const bool live = kb < skv;
     kb = live ? kb : 0;
-    const i32x4 rk = make_rsrc(kbase_ptr + (size_t)kb * D, live ? (uint32_t)(skv - kb) * D : 0u);
-    const i32x4 rv = make_rsrc(vbase_ptr + kb, live ? (uint32_t)D * a.ldv - (uint32_t)kb : 0u);
-    char* kl = lds + buf * TILE;
-    char* vl = lds + (2 + buf) * TILE;
+    Copy c;
+    c.rk = make_rsrc(kbase_ptr + (size_t)kb * D, live ? (uint32_t)(skv - kb) * D : 0u);
+    c.rv = make_rsrc(vbase_ptr + kb, live ? (uint32_t)D * a.ldv - (uint32_t)kb : 0u);
+    c.kl = lds + buf * TILE;
+    c.vl = lds + (2 + buf) * TILE;
+    return c;
+  };
+  auto issue_one = [&](const Copy& c, int i) {
+    if (i < IPW) dma16(c.rk, dma_off_k[i], c.kl + (w * IPW + i) * 1024);
+    else dma16(c.rv, dma_off_v[i - IPW], c.vl + (w * IPW + i - IPW) * 1024);
+  };
+  auto issue = [&](int kb, int buf) {
+    const Copy c = issue_plan(kb, buf);
 #pragma unroll
-    for (int u = 0; u < IPW; ++u) {
-      dma16(rk, dma_off_k[u], kl + (w * IPW + u) * 1024);
-      dma16(rv, dma_off_v[u], vl + (w * IPW + u) * 1024);
-    }
+    for (int u = 0; u < 2 * IPW; ++u) issue_one(c, u);
   };
   // E8M0 codes of the K and V blocks holding key kb (wave-uniform)
   const int* ksc = reinterpret_cast<const int*>(a.k_scale) + (size_t)kvh * nkb;
@@ -259,24 +268,23 @@ void fwd_fp8_kernel(Fp8FwdArgs a) {
   };
 
   const int n_full = walk.count_full();
-  int kb_next = 0;
-  TileRef ref_next{0, 0, 0};
-  if (n_it > 0) {
-    kb_next = walk.kbase(walk.fetch(0));
-    issue(kb_next, 0);
-    if (n_it > 1) ref_next = walk.fetch(1);
-  }
+  const int sub_log2 = log2_if_pow2(walk.sub);
+  KvTab tab;
+  auto kbase_of = [&](int it) { return tab.kbase(walk, it, sub_log2, lane); };
+  if (n_it > 0) issue(kbase_of(0), 0);
   wait_vmem();
   __syncthreads();
   auto tile_step = [&](int it, auto buf_c) {
     constexpr int buf = decltype(buf_c)::value;
-    const int kbase = kb_next;
+    const int kbase = kbase_of(it);
     bool masked = it >= n_full;
-    if (it + 1 < n_it) {
-      kb_next = walk.kbase(ref_next);
-      issue(kb_next, buf ^ 1);
+    const bool more = it + 1 < n_it;
+    Copy nc;
+    if (more) nc = issue_plan(kbase_of(it + 1), buf ^ 1);
+    if (kbase >= skv && more) {
+#pragma unroll
+      for (int i = 0; i < 2 * IPW; ++i) issue_one(nc, i);
     }
-    if (it + 2 < n_it) ref_next = walk.fetch(it + 2);
     if (kbase < skv) {  // workgroup-uniform
       masked = masked || (kbase + BN > skv);
       const char* kl = lds + buf * TILE;
@@ -286,6 +294,7 @@ void fwd_fp8_kernel(Fp8FwdArgs a) {
       const int scv = (scalar_load(vsc, kblk) >> 23) & 0xff;
 
       f32x16 sacc[2];
+      __builtin_amdgcn_s_setprio(1);  // MFMA phases first in issue order (4 % at C2, measured)
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
 #pragma unroll
@@ -296,8 +305,13 @@ void fwd_fp8_kernel(Fp8FwdArgs a) {
           const i32x8 kf = cat8(*reinterpret_cast<const u32x4*>(kr + koff[s][0]),
                                 *reinterpret_cast<const u32x4*>(kr + koff[s][1]));
           sacc[j] = mma_f8(kf, qf[s], sacc[j], sck, scq);
+          // this step's share of the next tile's copies
+#pragma unroll
+          for (int i = 0; i < 2 * IPW; ++i)
+            if (i * 2 * KS / (2 * IPW) == j * KS + s && more) issue_one(nc, i);
         }
       }
+      __builtin_amdgcn_s_setprio(0);
       if constexpr (kMods) {
 #pragma unroll
         for (int j = 0; j < 2; ++j)
@@ -319,6 +333,7 @@ void fwd_fp8_kernel(Fp8FwdArgs a) {
       }
       i32x8 pf;
       softmax(sacc, pf);
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int i = 0; i < DT; ++i) {
         const char* vr = vl + i * 32 * BN;
@@ -326,6 +341,7 @@ void fwd_fp8_kernel(Fp8FwdArgs a) {
                               *reinterpret_cast<const u32x4*>(vr + voff[1]));
         oacc[i] = mma_f8(vf, pf, oacc[i], scv, 127);
       }
+      __builtin_amdgcn_s_setprio(0);
     }
     wait_vmem();
     __syncthreads();
