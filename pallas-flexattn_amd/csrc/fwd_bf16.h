@@ -7,8 +7,9 @@
 // Per kv tile of BN keys (double-buffered in LDS, one barrier per tile):
 //   * K and V tiles are copied HBM -> LDS with buffer_load ... lds (no
 //     registers, no bounds branches: rows past the sequence read as zero),
-//     issued one tile ahead; block-table entries come through the scalar cache;
-//   * S^T = K Q^T   (A = K rows from LDS in perm23 order, fetched one k-step
+//     issued one tile ahead and spread over the S phase; the block-table row
+//     sits in a register (KvTab), so tiles make no table loads;
+//   * S^T = K Q^T   (A = K rows from LDS in perm23 order, fetched two k-steps
 //     ahead of the MFMAs; B = Q from VGPRs);
 //   * online softmax with one query per lane, speculative: exponentials
 //     against the current reference maximum, no per-tile maximum; only a lane
