@@ -109,6 +109,9 @@ PACK_CASES = [
     ("pack-16q-g4-window", 1, 8, 2, 16, 3000, 128, "window", None, 5),
     ("pack-4q-g4-alibi-cap", 2, 8, 2, 4, 2048, 64, None, "mods", None),
     ("pack-8q-g2-docs", 2, 4, 2, 8, 1200, 128, "docs-short", None, 3),
+    # g * Sq = 32 rows: the one-wave split-KV instance at its limit; 36 rows: the 4-wave tiles
+    ("pack-8q-g4-32rows", 1, 8, 2, 8, 2500, 128, None, None, 4),
+    ("pack-9q-g4-36rows", 1, 8, 2, 9, 2500, 128, None, None, 4),
 ]
 
 
