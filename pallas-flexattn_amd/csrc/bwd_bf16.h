@@ -267,12 +267,34 @@ void dq_bf16_kernel(BwdArgs a) {
       else mma_rows2<D>(rt, kl, vl, j, qf, df, sacc, pacc);
       __builtin_amdgcn_s_setprio(0);
       float dsdx[16];
+      if constexpr (kMods && !Mod::kScore) {
+        // built-in ALiBi + soft-cap: slope (k - q) = sb + slope c_e, the
+        // soft-cap's tanh as one exp2, one rcp and FMAs (wave-uniform branch)
+        const float sb = slope * (float)(kbase + 32 * j + 8 * hh - qw);
+        if (P.softcap > 0.f) {
+          const float c2 = 2.0f * kLog2e * cap_inv, capl2 = P.softcap * kLog2e;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        dsdx[e] = 1.f;
-        if constexpr (kMods)
-          sacc[e] = mod_score_flat<Mod>(P, sacc[e], slope, b, h, qw, kbase + 32 * j + acc_row(e, hh), cap_inv,
-                                    &dsdx[e]);
+          for (int e = 0; e < 16; ++e) {
+            const float sv = fmaf(sacc[e], P.scale, fmaf(slope, (float)acc_row(e, 0), sb));
+            const float th = fmaf(-2.0f, fast_rcp(fast_exp2(sv * c2) + 1.0f), 1.0f);
+            sacc[e] = capl2 * th;
+            dsdx[e] = fmaf(-th, th, 1.0f);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            sacc[e] = fmaf(sacc[e], P.scale, fmaf(slope, (float)acc_row(e, 0), sb)) * kLog2e;
+            dsdx[e] = 1.f;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          dsdx[e] = 1.f;
+          if constexpr (kMods)
+            sacc[e] = mod_score_flat<Mod>(P, sacc[e], slope, b, h, qw, kbase + 32 * j + acc_row(e, hh), cap_inv,
+                                      &dsdx[e]);
+        }
       }
       if constexpr (kMasked) {
 #pragma unroll
@@ -591,11 +613,27 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
     // and the bf16 packing once a half of the sub-tile is complete).
     float pvq[8][2], dsq[8][2];
     const float cap_inv = P.softcap > 0.f ? 1.0f / P.softcap : 0.f;
+    // built-in mods: the lane's ALiBi offset per sub-tile and the soft-cap constants
+    float asb[2] = {0.f, 0.f}, mc2 = 0.f, mcapl2 = 0.f;
+    if constexpr (kMods && !Mod::kScore) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) asb[j] = slope * (float)(kw - (qbase + 32 * j + 8 * hh));
+      mc2 = 2.0f * kLog2e * cap_inv;
+      mcapl2 = P.softcap * kLog2e;
+    }
     auto e_exp = [&](int j, int p) {
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int e = 2 * p + i, q = e >> 2;
-        if constexpr (kMods) {
+        if constexpr (kMods && !Mod::kScore) {
+          // built-in ALiBi + soft-cap (branch-free: both results, selected):
+          // slope (k - q) = asb[j] - slope c_e, tanh as one exp2 and one rcp
+          const float sv = fmaf(sacc[j][e], P.scale, fmaf(-slope, (float)acc_row(e, 0), asb[j]));
+          const float th = fmaf(-2.0f, fast_rcp(fast_exp2(sv * mc2) + 1.0f), 1.0f);
+          const bool capped = P.softcap > 0.f;
+          dsq[p][i] = capped ? fmaf(-th, th, 1.0f) : 1.0f;
+          pvq[p][i] = fast_exp2((capped ? mcapl2 * th : sv * kLog2e) + ls[j][q][e & 3]);
+        } else if constexpr (kMods) {
           // score mods (log2-domain logit) and d s / d(scale q.k) for dS
           const float t = mod_score_flat<Mod>(P, sacc[j][e], slope, b, hq, qbase + 32 * j + acc_row(e, hh), kw,
                                               cap_inv, &dsq[p][i]);

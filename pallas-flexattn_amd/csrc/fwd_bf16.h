@@ -339,7 +339,29 @@ void fwd_bf16_kernel(FwdArgs a) {
       }
       if (FA_FWD_PRIO) __builtin_amdgcn_s_setprio(0);
 
-      if constexpr (kMods) {
+      if constexpr (kMods && !Mod::kScore) {
+        // built-in ALiBi + soft-cap: slope (k - q) = slope (base_j + c_e) with
+        // base_j the lane's key offset of sub-tile j and c_e a constant, so
+        // two FMAs per element; the soft-cap's tanh folded into one exp2, one
+        // rcp and two FMAs, in a wave-uniform branch
+        const float c2 = 2.0f * kLog2e * cap_inv, capl2 = P.softcap * kLog2e;
+#pragma unroll
+        for (int j = 0; j < NSUB; ++j) {
+          const float sb = slope * (float)(kbase + 32 * j + 8 * hh - qw);
+          if (P.softcap > 0.f) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const float sv = fmaf(sacc[j][e], P.scale, fmaf(slope, (float)acc_row(e, 0), sb));
+              const float r = fast_rcp(fast_exp2(sv * c2) + 1.0f);
+              sacc[j][e] = fmaf(-2.0f * capl2, r, capl2);
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+              sacc[j][e] = fmaf(sacc[j][e], P.scale, fmaf(slope, (float)acc_row(e, 0), sb)) * kLog2e;
+          }
+        }
+      } else if constexpr (kMods) {
 #pragma unroll
         for (int j = 0; j < NSUB; ++j)
 #pragma unroll

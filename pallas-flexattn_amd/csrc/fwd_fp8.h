@@ -313,14 +313,23 @@ void fwd_fp8_kernel(Fp8FwdArgs a) {
       }
       __builtin_amdgcn_s_setprio(0);
       if constexpr (kMods) {
+        // ALiBi + soft-cap as in the bf16 forward: slope (k - q) = sb + slope e,
+        // tanh as one exp2 and one rcp, a wave-uniform soft-cap branch
+        const float c2 = 2.0f * kLog2e * cap_inv, capl2 = P.softcap * kLog2e;
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 2; ++j) {
+          const float sb = slope * (float)(kbase + 32 * j + 16 * hh - qw);
+          if (P.softcap > 0.f) {
 #pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            float dsdx;  // unused in the forward
-            sacc[j][e] = mod_score_flat<BuiltinMod>(P, sacc[j][e], slope, b, h, qw, kbase + 32 * j + 16 * hh + e,
-                                                    cap_inv, &dsdx);
+            for (int e = 0; e < 16; ++e) {
+              const float sv = fmaf(sacc[j][e], P.scale, fmaf(slope, (float)e, sb));
+              sacc[j][e] = fmaf(-2.0f * capl2, fast_rcp(fast_exp2(sv * c2) + 1.0f), capl2);
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) sacc[j][e] = fmaf(sacc[j][e], P.scale, fmaf(slope, (float)e, sb)) * kLog2e;
           }
+        }
       }
       if (masked) {  // partial tile: keys outside [klo, khi] are dropped
 #pragma unroll
