@@ -502,7 +502,8 @@ def emit(e: Expr) -> str:
         if e.dtype == "b":
             return "true" if e.value else "false"
         if e.dtype == "i":
-            return f"({e.value})"
+            # -2^31 written as a literal would be the negation of a long
+            return "(-2147483647 - 1)" if e.value == -2 ** 31 else f"({e.value})"
         v = e.value
         if math.isinf(v):
             return "(INFINITY)" if v > 0 else "(-INFINITY)"

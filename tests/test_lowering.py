@@ -40,6 +40,11 @@ def test_integer_semantics_follow_python():
     np.testing.assert_array_equal(low(Q, K), ((d // 7) == -2) | ((d % -5) == -3))
     src = L.policy_source(low.expr, None)
     assert "um_ifloordiv" in src and "um_imod" in src
+    # the smallest int32 stays an int literal in C++ (a bare -2147483648 is
+    # the negation of a long)
+    assert L.emit(L.const(-2 ** 31)) == "(-2147483647 - 1)"
+    low = L.lower_mask(lambda q, kv: (q - kv) > -2 ** 31)
+    np.testing.assert_array_equal(low(Q, K), np.broadcast_to(True, (Q.shape[0], K.shape[1])))
 
 
 def test_captured_tensor_reads_and_batch_head_dependence():
