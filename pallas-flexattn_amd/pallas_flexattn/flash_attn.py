@@ -349,8 +349,22 @@ def _tables_for(mask, mods, block_mask, q, k, tiles):
     return None, tiles
 
 
+_RAW_STREAM = None
+
+
 def _stream():
-    return _torch().cuda.current_stream().cuda_stream
+    """Handle of torch's current stream on the current device.  torch's
+    current_stream() builds a Stream object per call (~20 us); the raw
+    handle getters it wraps are used directly where present."""
+    global _RAW_STREAM
+    if _RAW_STREAM is None:
+        c = _torch()._C
+        if hasattr(c, "_cuda_getCurrentRawStream") and hasattr(c, "_cuda_getDevice"):
+            get, dev = c._cuda_getCurrentRawStream, c._cuda_getDevice
+            _RAW_STREAM = lambda: get(dev())  # noqa: E731
+        else:
+            _RAW_STREAM = lambda: _torch().cuda.current_stream().cuda_stream  # noqa: E731
+    return _RAW_STREAM()
 
 
 def _dense16(t):

@@ -12,6 +12,7 @@ from typing import NamedTuple, Optional
 
 from . import _lib
 from .block_mask import BlockMask
+from .flash_attn import _stream
 from .kernel_tuner import DEFAULT_TILES
 
 SCALE_ROWS = 128  # rows per scale block
@@ -52,7 +53,7 @@ def quantize_fp8(x, transpose: bool = False) -> Fp8Tensor:
     scale = torch.empty((B, H, nb), device=x.device, dtype=torch.float32)
     lib = _lib.load()
     _lib.check(lib.fa_quantize_fp8(x.data_ptr(), B * H, S, D, int(transpose), out.data_ptr(), scale.data_ptr(),
-                                   torch.cuda.current_stream().cuda_stream))
+                                   _stream()))
     return Fp8Tensor(out, scale, S, bool(transpose))
 
 
@@ -104,9 +105,8 @@ class Fp8Runner:
         self.lib = _lib.load()
 
     def fwd(self):
-        import torch
         _lib.check(self.lib.fa_fwd_fp8(self.plan.ptr(), _lib.ctypes.byref(self.args), self.o.data_ptr(),
-                                       self.lse.data_ptr(), torch.cuda.current_stream().cuda_stream))
+                                       self.lse.data_ptr(), _stream()))
 
 
 def _prepare(query, key, value, score_mod, block_mask, enable_gqa, resolve):
