@@ -19,7 +19,9 @@ plus the FlexAttention front door :func:`flex_attention` (``score_mod``,
 ``block_mask``, ``scale``, ``enable_gqa``, ``return_lse``, ``kernel_options``).
 
 ``interpret=True`` selected the Pallas interpreter on the host in the
-reference; this build has no host execution path and raises.
+reference; here it runs the library's host twins (``fa_fwd_host`` /
+``fa_bwd_*_host``) on CPU tensors.  Problems without queries or keys launch
+nothing: empty outputs, or O = 0 and LSE = -inf when there are no keys.
 """
 import math
 import os
@@ -386,6 +388,12 @@ def _fwd_core(q, k, v, mask, score, scale, block_mask, tiles, mods=None, host=Fa
     _check_inputs(q, k, v, host)
     if host:
         _host_mods(mods)
+    if q.numel() == 0 or k.shape[2] == 0:
+        # nothing to launch: no queries (empty outputs), or no keys (every
+        # row sees none: O = 0, LSE = -inf, as for fully masked rows)
+        o = torch.zeros_like(q)
+        lse = torch.full(q.shape[:3], -math.inf, device=q.device, dtype=torch.float32)
+        return o, lse, None
     q, k, v = _dense16(q), _dense16(k), _dense16(v)
     if mods is not None:
         tiles = _MODS_TILES[_dtype_code(q)[1]]
@@ -413,6 +421,8 @@ def _bwd_core(q, k, v, o, lse, do, mask, score, scale, block_mask, tiles, mods=N
     _check_inputs(q, k, v, host)
     if host:
         _host_mods(mods)
+    if q.numel() == 0 or k.shape[2] == 0:  # no (query, key) pair: zero gradients
+        return torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v)
     if do.dtype != q.dtype:
         do = do.to(q.dtype)
     q, k, v, o, do = (_dense16(t) for t in (q, k, v, o, do))

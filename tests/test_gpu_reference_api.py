@@ -247,3 +247,22 @@ def test_block_m64_tile(case):
         else:  # large logits: the algorithm's bf16 roundings set the error (see test_gpu_parity)
             assert_close(f"{n} vs float64", got[n], w, dict(atol=1e-1, rtol=1e-2))
             assert_as_accurate(n, got[n], tw, w)
+
+
+def test_empty_problems_launch_nothing():
+    """GPU tensors without queries give empty outputs and gradients; without
+    keys every row sees nothing: O = 0, LSE = -inf, zero gradients."""
+    import torch
+    import pallas_flexattn as pf
+    print("[gpu reference api] empty problems", flush=True)
+    x = torch.zeros(2, 2, 0, 64, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    o = pf.flash_attention(x, x, x, mask_mod=pf.causal_mask)
+    o.sum().backward()
+    assert o.shape == (2, 2, 0, 64) and x.grad.shape == x.shape
+    q = torch.randn(1, 4, 7, 64, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    kv = torch.zeros(1, 2, 0, 64, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    o, lse = pf.flex_attention(q, kv, kv, enable_gqa=True, return_lse=True)
+    o.sum().backward()
+    torch.cuda.synchronize()
+    assert not o.any() and bool(torch.isneginf(lse).all())
+    assert not q.grad.any() and kv.grad.shape == kv.shape

@@ -175,3 +175,25 @@ def test_host_path_refusals():
         pf.flash_attention(x, x, x)  # CPU tensors without interpret
     with pytest.raises(NotImplementedError, match="interpret=True"):
         pf.flash_attention(x, x, x, mask_mod=lambda q, k: (q - k) % 2 == 0, interpret=True)
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+def test_empty_problems_interpret(dtype):
+    """No queries: empty outputs and gradients.  No keys (Sq > 0): every row
+    sees nothing, O = 0 and LSE = -inf (the fully-masked-row convention), zero
+    gradients."""
+    td = torch.float32 if dtype == "fp32" else torch.bfloat16
+    x = torch.zeros(2, 2, 0, 32, dtype=td, requires_grad=True)
+    o = pf.flash_attention(x, x, x, mask_mod=pf.causal_mask, interpret=True)
+    o.sum().backward()
+    assert o.shape == (2, 2, 0, 32) and x.grad.shape == x.shape
+    o, lse = pf.flash_attention_fwd(x.detach(), x.detach(), x.detach(), interpret=True)
+    assert o.shape == (2, 2, 0, 32) and lse.shape == (2, 2, 0)
+    q = torch.randn(1, 2, 5, 32, dtype=td, requires_grad=True)
+    kv = torch.zeros(1, 2, 0, 32, dtype=td, requires_grad=True)
+    from pallas_flexattn.flash_attn import _bwd_core, _fwd_core
+    o, lse, _ = _fwd_core(q.detach(), kv.detach(), kv.detach(), None, None, None, None, (128, 64, 128), None, True)
+    assert torch.equal(o, torch.zeros_like(o)) and bool(torch.isneginf(lse).all())
+    dq, dk, dv = _bwd_core(q.detach(), kv.detach(), kv.detach(), o, lse, torch.ones_like(o), None, None, None, None,
+                           (128, 64, 128), None, True)
+    assert not dq.any() and dk.shape == kv.shape and dv.shape == kv.shape
