@@ -224,8 +224,15 @@ void fwd_bf16_kernel(FwdArgs a) {
   // Exponentials of a whole tile against reference muse, into the bf16
   // fragments pf; returns the lane's float32 sum.  Without score mods sacc
   // keeps raw (masked) q.k: the max is taken on it (scale > 0) and the scale
-  // is folded into the exponent's FMA.  With mods sacc holds log2-domain
-  // logits.
+  // is folded into the exponent's FMA.  With mods sacc holds y with the
+  // log2-domain logit ea * y + eb: the logit itself (ea = 1, eb = 0), or with
+  // the built-in soft-cap r = 1 / (2^(2 s log2(e) / cap) + 1), whose logit is
+  // cap log2(e) tanh(s / cap) = cap log2(e) (1 - 2 r) (ea = -2 cap log2(e),
+  // eb = cap log2(e)): the exponent is one FMA either way.  Masked elements
+  // hold the y whose logit is -inf (-inf, or +inf for r).
+  const bool rform = kMods && !Mod::kScore && P.softcap > 0.f;
+  const float ea = rform ? -2.0f * P.softcap * kLog2e : 1.0f;
+  const float eb = rform ? P.softcap * kLog2e : 0.0f;
   auto exps = [&](const f32x16* sacc, frag* pf, float muse) {
     float rs0 = 0.f, rs1 = 0.f;
 #pragma unroll
@@ -234,7 +241,7 @@ void fwd_bf16_kernel(FwdArgs a) {
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
         const float s = sacc[c >> 1][8 * (c & 1) + t];
-        if constexpr (kMods) x[t] = fast_exp2(s - muse);
+        if constexpr (kMods) x[t] = fast_exp2(fmaf(s, ea, eb - muse));
         else x[t] = fast_exp2(fmaf(s, P.scale_log2, -muse));
       }
       pf[c] = E::pack(x);
@@ -253,9 +260,10 @@ void fwd_bf16_kernel(FwdArgs a) {
 #pragma unroll
       for (int j = 0; j < NSUB; ++j)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sacc[j][e]);
+        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, kMods ? sacc[j][e] * ea : sacc[j][e]);
       float mt = pair_max(mx);
       if constexpr (!kMods) mt *= P.scale_log2;
+      else mt += eb;
       const float mnew = fmaxf(m, mt);
       if (__any(mnew > m)) {
         const float alpha = fast_exp2(m - (mnew == -INFINITY ? 0.f : mnew));
@@ -342,19 +350,18 @@ void fwd_bf16_kernel(FwdArgs a) {
       if constexpr (kMods && !Mod::kScore) {
         // built-in ALiBi + soft-cap: slope (k - q) = slope (base_j + c_e) with
         // base_j the lane's key offset of sub-tile j and c_e a constant, so
-        // two FMAs per element; the soft-cap's tanh folded into one exp2, one
-        // rcp and two FMAs, in a wave-uniform branch
-        const float c2 = 2.0f * kLog2e * cap_inv, capl2 = P.softcap * kLog2e;
+        // two FMAs per element; with the soft-cap (a wave-uniform branch) the
+        // tanh's factor 2 log2(e) / cap is folded into those FMAs and the
+        // tile keeps r = 1 / (2^t + 1) (see exps): one exp2, one add, one rcp
+        const float c2 = 2.0f * kLog2e * cap_inv;
 #pragma unroll
         for (int j = 0; j < NSUB; ++j) {
           const float sb = slope * (float)(kbase + 32 * j + 8 * hh - qw);
           if (P.softcap > 0.f) {
+            const float a2 = P.scale * c2, sl2 = slope * c2, sb2 = sb * c2;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-              const float sv = fmaf(sacc[j][e], P.scale, fmaf(slope, (float)acc_row(e, 0), sb));
-              const float r = fast_rcp(fast_exp2(sv * c2) + 1.0f);
-              sacc[j][e] = fmaf(-2.0f * capl2, r, capl2);
-            }
+            for (int e = 0; e < 16; ++e)
+              sacc[j][e] = fast_rcp(fast_exp2(fmaf(sacc[j][e], a2, fmaf(sl2, (float)acc_row(e, 0), sb2))) + 1.0f);
           } else {
 #pragma unroll
             for (int e = 0; e < 16; ++e)
@@ -372,12 +379,13 @@ void fwd_bf16_kernel(FwdArgs a) {
           }
       }
       if (masked) {  // partial tile: keys outside [klo, khi] are dropped
+        const float dead = rform ? INFINITY : -INFINITY;  // the y whose logit is -inf
 #pragma unroll
         for (int j = 0; j < NSUB; ++j)
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             const int key = kbase + 32 * j + acc_row(e, hh);
-            sacc[j][e] = mod_keep<Mod>(P, b, h, qw, key, klo, khi) ? sacc[j][e] : -INFINITY;
+            sacc[j][e] = mod_keep<Mod>(P, b, h, qw, key, klo, khi) ? sacc[j][e] : dead;
           }
       }
       // V^T fragments of d tile i (two tiles in flight): tile 0's reads issue
