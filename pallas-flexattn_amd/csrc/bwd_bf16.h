@@ -202,6 +202,9 @@ void dq_bf16_kernel(BwdArgs a) {
   const float dl = qvalid ? a.delta[rowi] : 0.f;
   const float slope = P.alibi ? P.alibi[h] : 0.f;
   const float cap_inv = P.softcap > 0.f ? 1.0f / P.softcap : 0.f;
+  // with mods a tile holds y with the log2-domain logit ea * y: the logit
+  // itself, or with the built-in soft-cap tanh(s / cap) (ea = cap log2(e))
+  const float ea = (kMods && !Mod::kScore && P.softcap > 0.f) ? P.softcap * kLog2e : 1.0f;
   int klo, khi;  // keys visible to this lane's query (masks are intervals here)
   key_interval(P, b, qw, &klo, &khi);
 
@@ -270,14 +273,17 @@ void dq_bf16_kernel(BwdArgs a) {
       if constexpr (kMods && !Mod::kScore) {
         // built-in ALiBi + soft-cap: slope (k - q) = sb + slope c_e, the
         // soft-cap's tanh as one exp2, one rcp and FMAs (wave-uniform branch)
+        // with its factor 2 log2(e) / cap folded into the score FMAs; the
+        // tile keeps tanh itself (the logit is ea tanh, see below)
         const float sb = slope * (float)(kbase + 32 * j + 8 * hh - qw);
         if (P.softcap > 0.f) {
-          const float c2 = 2.0f * kLog2e * cap_inv, capl2 = P.softcap * kLog2e;
+          const float c2 = 2.0f * kLog2e * cap_inv;
+          const float a2 = P.scale * c2, sl2 = slope * c2, sb2 = sb * c2;
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
-            const float sv = fmaf(sacc[e], P.scale, fmaf(slope, (float)acc_row(e, 0), sb));
-            const float th = fmaf(-2.0f, fast_rcp(fast_exp2(sv * c2) + 1.0f), 1.0f);
-            sacc[e] = capl2 * th;
+            const float th =
+                fmaf(-2.0f, fast_rcp(fast_exp2(fmaf(sacc[e], a2, fmaf(sl2, (float)acc_row(e, 0), sb2))) + 1.0f), 1.0f);
+            sacc[e] = th;
             dsdx[e] = fmaf(-th, th, 1.0f);
           }
         } else {
@@ -306,7 +312,7 @@ void dq_bf16_kernel(BwdArgs a) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         float pv;
-        if constexpr (kMods) pv = fast_exp2(sacc[e] - lse2);
+        if constexpr (kMods) pv = fast_exp2(fmaf(sacc[e], ea, -lse2));
         else pv = fast_exp2(fmaf(sacc[e], P.scale_log2, -lse2));
         if constexpr (kMods) pacc[e] = pv * (pacc[e] - dl) * dsdx[e];
         else pacc[e] = pv * (pacc[e] - dl);
@@ -614,12 +620,18 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
     float pvq[8][2], dsq[8][2];
     const float cap_inv = P.softcap > 0.f ? 1.0f / P.softcap : 0.f;
     // built-in mods: the lane's ALiBi offset per sub-tile and the soft-cap constants
-    float asb[2] = {0.f, 0.f}, mc2 = 0.f, mcapl2 = 0.f;
+    // with the score's factor f (2 log2(e) / cap with the soft-cap, log2(e)
+    // without) folded into the lane's ALiBi base, the slope and the scale
+    float asb[2] = {0.f, 0.f}, msl = 0.f, msc = 0.f, mea = 1.0f;
+    bool capped = false;
     if constexpr (kMods && !Mod::kScore) {
+      capped = P.softcap > 0.f;
+      const float f = capped ? 2.0f * kLog2e * cap_inv : kLog2e;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) asb[j] = slope * (float)(kw - (qbase + 32 * j + 8 * hh));
-      mc2 = 2.0f * kLog2e * cap_inv;
-      mcapl2 = P.softcap * kLog2e;
+      for (int j = 0; j < 2; ++j) asb[j] = f * slope * (float)(kw - (qbase + 32 * j + 8 * hh));
+      msl = -f * slope;
+      msc = f * P.scale;
+      mea = capped ? P.softcap * kLog2e : 1.0f;
     }
     auto e_exp = [&](int j, int p) {
 #pragma unroll
@@ -627,12 +639,12 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
         const int e = 2 * p + i, q = e >> 2;
         if constexpr (kMods && !Mod::kScore) {
           // built-in ALiBi + soft-cap (branch-free: both results, selected):
-          // slope (k - q) = asb[j] - slope c_e, tanh as one exp2 and one rcp
-          const float sv = fmaf(sacc[j][e], P.scale, fmaf(-slope, (float)acc_row(e, 0), asb[j]));
-          const float th = fmaf(-2.0f, fast_rcp(fast_exp2(sv * mc2) + 1.0f), 1.0f);
-          const bool capped = P.softcap > 0.f;
+          // u = f (scale q.k + slope (k - q)); tanh(s / cap) = 1 - 2 / (2^u + 1)
+          // as one exp2 and one rcp; the logit is cap log2(e) tanh, or u
+          const float u = fmaf(sacc[j][e], msc, fmaf(msl, (float)acc_row(e, 0), asb[j]));
+          const float th = fmaf(-2.0f, fast_rcp(fast_exp2(u) + 1.0f), 1.0f);
           dsq[p][i] = capped ? fmaf(-th, th, 1.0f) : 1.0f;
-          pvq[p][i] = fast_exp2((capped ? mcapl2 * th : sv * kLog2e) + ls[j][q][e & 3]);
+          pvq[p][i] = fast_exp2(fmaf(mea, capped ? th : u, ls[j][q][e & 3]));
         } else if constexpr (kMods) {
           // score mods (log2-domain logit) and d s / d(scale q.k) for dS
           const float t = mod_score_flat<Mod>(P, sacc[j][e], slope, b, hq, qbase + 32 * j + acc_row(e, hh), kw,
