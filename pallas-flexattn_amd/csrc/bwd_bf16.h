@@ -286,10 +286,11 @@ void dq_bf16_kernel(BwdArgs a) {
             sacc[e] = th;
             dsdx[e] = fmaf(-th, th, 1.0f);
           }
-        } else {
+        } else {  // log2(e) folded in the same way
+          const float al = P.scale * kLog2e, sll = slope * kLog2e, sbl = sb * kLog2e;
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
-            sacc[e] = fmaf(sacc[e], P.scale, fmaf(slope, (float)acc_row(e, 0), sb)) * kLog2e;
+            sacc[e] = fmaf(sacc[e], al, fmaf(sll, (float)acc_row(e, 0), sbl));
             dsdx[e] = 1.f;
           }
         }

@@ -362,10 +362,10 @@ void fwd_bf16_kernel(FwdArgs a) {
 #pragma unroll
             for (int e = 0; e < 16; ++e)
               sacc[j][e] = fast_rcp(fast_exp2(fmaf(sacc[j][e], a2, fmaf(sl2, (float)acc_row(e, 0), sb2))) + 1.0f);
-          } else {
+          } else {  // log2(e) folded in the same way
+            const float al = P.scale * kLog2e, sll = slope * kLog2e, sbl = sb * kLog2e;
 #pragma unroll
-            for (int e = 0; e < 16; ++e)
-              sacc[j][e] = fmaf(sacc[j][e], P.scale, fmaf(slope, (float)acc_row(e, 0), sb)) * kLog2e;
+            for (int e = 0; e < 16; ++e) sacc[j][e] = fmaf(sacc[j][e], al, fmaf(sll, (float)acc_row(e, 0), sbl));
           }
         }
       } else if constexpr (kMods) {

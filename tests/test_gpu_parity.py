@@ -41,6 +41,9 @@ CASES = [
     ("dense-fp32-d32", "fp32", 1, 2, 2, 128, 32, ("none",), {}),
     ("causal-bf16-d32", "bf16", 1, 2, 2, 256, 32, ("causal",), {}),
     ("softcap-fp32-d128", "fp32", 1, 2, 1, 160, 128, ("causal",), {"softcap": 20.0, "alibi": True}),
+    # each built-in score mod alone (the kernels' uncapped and capped branches)
+    ("gqa-alibi-only-bf16", "bf16", 1, 4, 2, 320, 128, ("causal",), {"alibi": True}),
+    ("softcap-only-window-bf16-d64", "bf16", 2, 2, 2, 384, 64, ("window", 96, 16), {"softcap": 30.0}),
     # full tiles of several q heads walked before the partial ones (GQA group of 4, no score mods)
     ("gqa-causal-bf16-d128", "bf16", 2, 8, 2, 384, 128, ("causal",), {}),
     # a window wide enough for fully-live tiles inside it
