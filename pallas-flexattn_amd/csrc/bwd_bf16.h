@@ -262,7 +262,8 @@ void dq_bf16_kernel(BwdArgs a) {
     for (int j = 0; j < NSUB; ++j) {
       f32x16 sacc, pacc;
       zero(sacc);
-      zero(pacc);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) pacc[e] = dl;  // Delta - dP after the MFMAs (dO negated)
       // MFMA phases at raised wave priority, so the SIMD's other wave runs its
       // exponentials beside them (2.5 % at C2, measured)
       __builtin_amdgcn_s_setprio(1);
@@ -315,8 +316,8 @@ void dq_bf16_kernel(BwdArgs a) {
         float pv;
         if constexpr (kMods) pv = fast_exp2(fmaf(sacc[e], ea, -lse2));
         else pv = fast_exp2(fmaf(sacc[e], P.scale_log2, -lse2));
-        if constexpr (kMods) pacc[e] = pv * (pacc[e] - dl) * dsdx[e];
-        else pacc[e] = pv * (pacc[e] - dl);
+        if constexpr (kMods) pacc[e] = -pv * pacc[e] * dsdx[e];
+        else pacc[e] = -pv * pacc[e];
       }
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
@@ -355,6 +356,12 @@ void dq_bf16_kernel(BwdArgs a) {
   // complete on every path into the loop
   wait_vmem();
   __syncthreads();
+  // dO is kept negated (bf16 sign flips), so the dP^T MFMA accumulates -dP
+  // onto its starting value: started from Delta it gives Delta - dP, and
+  // dS = -P (Delta - dP) takes one multiply per element
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int s = 0; s < KSTEPS; ++s) df[s] ^= 0x80008000u;
   // (the buffer index stays a run-time value here: as a constant it costs
   // this 256-VGPR kernel spills)
   // the next tile's copies are spread over the first sub-tile's k steps (as
