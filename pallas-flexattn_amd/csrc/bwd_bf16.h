@@ -305,10 +305,15 @@ void dq_bf16_kernel(BwdArgs a) {
         }
       }
       if constexpr (kMasked) {
+        // key kbase + 32 j + acc_row(e, hh), compared against tile-relative
+        // bounds (a constant per element)
+        const int lo = klo - kbase - 32 * j - 8 * hh, hi = khi - kbase - 32 * j - 8 * hh;
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const int key = kbase + 32 * j + acc_row(e, hh);
-          sacc[e] = mod_keep<Mod>(P, b, h, qw, key, klo, khi) ? sacc[e] : -INFINITY;
+          const int c = acc_row(e, 0);
+          bool keep = c >= lo && c <= hi;
+          if constexpr (Mod::kMask) keep = keep && Mod::mask(P, b, h, qw, kbase + 32 * j + c + 8 * hh);
+          sacc[e] = keep ? sacc[e] : -INFINITY;
         }
       }
 #pragma unroll

@@ -380,12 +380,17 @@ void fwd_bf16_kernel(FwdArgs a) {
       }
       if (masked) {  // partial tile: keys outside [klo, khi] are dropped
         const float dead = rform ? INFINITY : -INFINITY;  // the y whose logit is -inf
+        // key kbase + c_e with c_e = 32 j + acc_row(e, hh): the bounds are
+        // taken relative to the tile, so each element compares a constant
+        const int lo = klo - kbase - 8 * hh, hi = khi - kbase - 8 * hh;
 #pragma unroll
         for (int j = 0; j < NSUB; ++j)
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
-            const int key = kbase + 32 * j + acc_row(e, hh);
-            sacc[j][e] = mod_keep<Mod>(P, b, h, qw, key, klo, khi) ? sacc[j][e] : dead;
+            const int c = 32 * j + acc_row(e, 0);
+            bool keep = c >= lo && c <= hi;
+            if constexpr (Mod::kMask) keep = keep && Mod::mask(P, b, h, qw, kbase + c + 8 * hh);
+            sacc[j][e] = keep ? sacc[j][e] : dead;
           }
       }
       // V^T fragments of d tile i (two tiles in flight): tile 0's reads issue
