@@ -367,14 +367,14 @@ void dq_bf16_kernel(BwdArgs a) {
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int s = 0; s < KSTEPS; ++s) df[s] ^= 0x80008000u;
-  // (the buffer index stays a run-time value here: as a constant it costs
-  // this 256-VGPR kernel spills)
+  // (the buffer index is a compile-time constant, tiles run in pairs, so
+  // LDS operand addresses fold into immediate offsets)
   // the next tile's copies are spread over the first sub-tile's k steps (as
   // in the forward: issued back to back they queue at the texture unit;
   // 0.7 % of this kernel at S = 8192, measured)
   constexpr int IPW = TileDma<D, BN, NW>::IPW;
-  auto step = [&](int it, auto masked_c) {
-    const int buf = it & 1;
+  auto step = [&](int it, auto masked_c, auto buf_c) {
+    constexpr int buf = decltype(buf_c)::value;  // == it & 1
     const int kbase = kb_next;
     const bool more = it + 1 < n_it;
     i32x4 rk = {0, 0, 0, 0}, rv = {0, 0, 0, 0};
@@ -404,9 +404,8 @@ void dq_bf16_kernel(BwdArgs a) {
     __syncthreads();
   };
   const int n_full = walk.count_full();
-  int it = 0;
-  for (; it < n_full; ++it) step(it, False{});
-  for (; it < n_it; ++it) step(it, True{});
+  run_tiles(0, n_full, step, False{});
+  run_tiles(n_full, n_it, step, True{});
 
 #pragma unroll
   for (int i = 0; i < DT; ++i) mfma_drain<'v'>(dqa[i]);
