@@ -82,8 +82,9 @@ __device__ __forceinline__ f32x16 mma_f8(i32x8 a, i32x8 b, f32x16 acc, int sa, i
 template <int D, int NW, bool kMods>
 // (three waves per SIMD: the 32 KiB of LDS allows five workgroups per CU, and
 // the third wave hides more of the softmax than the registers it takes cost:
-// 8 % faster than two at causal S = 8192)
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(occupancy_for(4 * 64 * D, NW, 3))))
+// 8 % faster than two at causal S = 8192; with score mods two, whose 256
+// registers hold the longer per-score chain without spilling)
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(occupancy_for(4 * 64 * D, NW, kMods ? 2 : 3))))
 void fwd_fp8_kernel(Fp8FwdArgs a) {
   constexpr int BN = 64;              // keys per tile
   constexpr int BM = 32 * NW;
@@ -218,6 +219,13 @@ void fwd_fp8_kernel(Fp8FwdArgs a) {
     for (int e = 0; e < 16; ++e) oacc[i][e] = 0.f;
   float m = -INFINITY, l = 0.f;
 
+  // With mods a tile holds y with the log2-domain logit ea * y + eb, as in
+  // the bf16 forward: the logit (ea = 1, eb = 0), or with the soft-cap
+  // r = 1 / (2^t + 1) (ea = -2 cap log2(e), eb = cap log2(e)); masked
+  // elements hold the y whose logit is -inf.
+  const bool rform = kMods && P.softcap > 0.f;
+  const float ea = rform ? -2.0f * P.softcap * kLog2e : 1.0f;
+  const float eb = rform ? P.softcap * kLog2e : 0.0f;
   // p * 2^kPBias of a whole tile against reference muse into the e4m3 operand
   // pf (element e of sub-tile j is byte 16 j + e); returns the lane's sum
   auto exps = [&](const f32x16* sacc, i32x8& pf, float muse) {
@@ -231,7 +239,7 @@ void fwd_fp8_kernel(Fp8FwdArgs a) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const float s = sacc[j][e + t];
-          if constexpr (kMods) x[t] = fast_exp2(s - mb);
+          if constexpr (kMods) x[t] = fast_exp2(fmaf(s, ea, eb - mb));
           else x[t] = fast_exp2(fmaf(s, P.scale_log2, -mb));
         }
         int word = __builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false);
@@ -249,9 +257,10 @@ void fwd_fp8_kernel(Fp8FwdArgs a) {
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sacc[j][e]);
+        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, kMods ? sacc[j][e] * ea : sacc[j][e]);
       float mt = pair_max(mx);
       if constexpr (!kMods) mt *= P.scale_log2;
+      else mt += eb;
       const float mnew = fmaxf(m, mt);
       if (__any(mnew > m)) {
         const float alpha = fast_exp2(m - (mnew == -INFINITY ? 0.f : mnew));
@@ -314,30 +323,33 @@ void fwd_fp8_kernel(Fp8FwdArgs a) {
       __builtin_amdgcn_s_setprio(0);
       if constexpr (kMods) {
         // ALiBi + soft-cap as in the bf16 forward: slope (k - q) = sb + slope e,
-        // tanh as one exp2 and one rcp, a wave-uniform soft-cap branch
-        const float c2 = 2.0f * kLog2e * cap_inv, capl2 = P.softcap * kLog2e;
+        // the score's factor (2 log2(e) / cap with the soft-cap, log2(e)
+        // without) folded into the FMAs; with the soft-cap the tile keeps
+        // r = 1 / (2^t + 1) (one exp2, one rcp), a wave-uniform branch
+        const float f = P.softcap > 0.f ? 2.0f * kLog2e * cap_inv : kLog2e;
+        const float af = P.scale * f, slf = slope * f;
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          const float sb = slope * (float)(kbase + 32 * j + 16 * hh - qw);
+          const float sbf = slope * (float)(kbase + 32 * j + 16 * hh - qw) * f;
           if (P.softcap > 0.f) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-              const float sv = fmaf(sacc[j][e], P.scale, fmaf(slope, (float)e, sb));
-              sacc[j][e] = fmaf(-2.0f * capl2, fast_rcp(fast_exp2(sv * c2) + 1.0f), capl2);
-            }
+            for (int e = 0; e < 16; ++e)
+              sacc[j][e] = fast_rcp(fast_exp2(fmaf(sacc[j][e], af, fmaf(slf, (float)e, sbf))) + 1.0f);
           } else {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) sacc[j][e] = fmaf(sacc[j][e], P.scale, fmaf(slope, (float)e, sb)) * kLog2e;
+            for (int e = 0; e < 16; ++e) sacc[j][e] = fmaf(sacc[j][e], af, fmaf(slf, (float)e, sbf));
           }
         }
       }
       if (masked) {  // partial tile: keys outside [klo, khi] are dropped
+        const float dead = rform ? INFINITY : -INFINITY;  // the y whose logit is -inf
+        const int lo = klo - kbase - 16 * hh, hi = khi - kbase - 16 * hh;  // tile-relative bounds
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
-            const int key = kbase + 32 * j + 16 * hh + e;
-            sacc[j][e] = (key >= klo && key <= khi) ? sacc[j][e] : -INFINITY;
+            const int c = 32 * j + e;
+            sacc[j][e] = (c >= lo && c <= hi) ? sacc[j][e] : dead;
           }
       }
       i32x8 pf;
