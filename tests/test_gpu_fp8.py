@@ -55,6 +55,8 @@ CASES = [
     ("window-d128", 1, 2, 2, 640, 640, 128, ("window", 100, 20), {}),
     ("doc-causal-d128", 2, 2, 2, 512, 512, 128, ("doc",), {}),
     ("gqa-alibi-softcap-d128", 1, 8, 2, 384, 384, 128, ("causal",), {"alibi": True, "softcap": 30.0}),
+    ("gqa-alibi-softcap-window-d64", 2, 4, 2, 320, 320, 64, ("window", 64, 0), {"alibi": True, "softcap": 20.0}),
+    ("alibi-only-d128", 1, 4, 4, 256, 256, 128, ("causal",), {"alibi": True}),
     ("cross-d128", 1, 2, 2, 256, 704, 128, ("none",), {}),
 ]
 
