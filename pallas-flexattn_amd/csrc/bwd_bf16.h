@@ -96,9 +96,10 @@ struct TileDma {
     row0 = row0 < rows ? row0 : rows;
     return make_rsrc(base + (size_t)row0 * RB, (uint32_t)(rows - row0) * RB);
   }
-  // the u-th of this wave's IPW copy instructions
+  // the u-th of this wave's IPW copy instructions (u a compile-time constant
+  // after unrolling; u = 0 is the descriptor's first use)
   __device__ __forceinline__ void one(const i32x4& rs, int u, char* lds_tile, int w) const {
-    dma16(rs, off[u], lds_tile + (w * IPW + u) * 1024);
+    dma16(rs, off[u], lds_tile + (w * IPW + u) * 1024, u == 0);
   }
   __device__ __forceinline__ void issue(const char* base, int row0, int rows, char* lds_tile, int w) const {
     const i32x4 rs = rsrc(base, row0, rows);

@@ -52,19 +52,33 @@ __device__ __forceinline__ u32x4 buf_load16(i32x4 rsrc, int byte_off) {
 // vmcnt waits stay correct: loads counted in order only complete later when
 // unknown copies are queued behind them.
 //
-// M0 is a register the compiler reserves, so the asm saves it in a scratch
-// SGPR and puts it back after the copy (the copy takes M0 when it issues).
-__device__ __forceinline__ void dma16(i32x4 rsrc, int byte_off, char* lds_wave_base) {
+// The copy's LDS base goes in M0, a register the compiler reserves: it is an
+// input operand bound to M0, so the compiler writes M0 itself right before the
+// asm (and knows its value afterwards); the asm only reads it.
+//
+// Wait states: a VMEM instruction that reads an SGPR written by a VALU
+// instruction (here the descriptor's v_readfirstlane) needs 5 wait states
+// after that write, and an LDS DMA needs 1 after an SALU write of M0.  The
+// compiler's hazard recognizer does not look inside inline asm, and it often
+// places the descriptor's readfirstlane a few instructions before the copy,
+// so the first copy through a new descriptor (`fresh`) provides all 5 itself
+// (s_nop 4), whatever precedes it.  Later copies through the same descriptor
+// come after that one (its SGPRs were written before it) and wait 1; the
+// static scan of the compiled kernels checks every copy on every path.
+__device__ __forceinline__ void dma16(i32x4 rsrc, int byte_off, char* lds_wave_base, bool fresh = true) {
   // the low 32 bits of a flat pointer into the shared aperture are the LDS
   // byte address
   const uint32_t m0v = __builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)lds_wave_base);
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(byte_off), "s"(rsrc), "s"(m0v)
-      : "memory");
+  if (fresh)
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                 :
+                 : "v"(byte_off), "s"(rsrc), "{m0}"(m0v)
+                 : "memory");
+  else
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                 :
+                 : "v"(byte_off), "s"(rsrc), "{m0}"(m0v)
+                 : "memory");
 }
 
 // s_waitcnt vmcnt(0) (expcnt, lgkmcnt left at their maxima) through the

@@ -200,8 +200,8 @@ void fwd_fp8_kernel(Fp8FwdArgs a) {
     return c;
   };
   auto issue_one = [&](const Copy& c, int i) {
-    if (i < IPW) dma16(c.rk, dma_off_k[i], c.kl + (w * IPW + i) * 1024);
-    else dma16(c.rv, dma_off_v[i - IPW], c.vl + (w * IPW + i - IPW) * 1024);
+    if (i < IPW) dma16(c.rk, dma_off_k[i], c.kl + (w * IPW + i) * 1024, i == 0);
+    else dma16(c.rv, dma_off_v[i - IPW], c.vl + (w * IPW + i - IPW) * 1024, i == IPW);
   };
   auto issue = [&](int kb, int buf) {
     const Copy c = issue_plan(kb, buf);

@@ -13,8 +13,11 @@ it (`s_nop N` counts N + 1, any other instruction 1), scanning each kernel in fa
 order.  In the other direction, an inline-asm MFMA must not read an A or B operand that a
 compiler-emitted VALU instruction wrote fewer than 2 wait states before (the schedules that drop
 `mfma_acc`'s leading `s_nop 1` rely on this).  M0 is a register the compiler reserves: an inline
-asm block that writes M0 (the LDS-DMA copy) must save it first and put the saved value back as its
-last M0 write.  Each scan is checked on a planted case."""
+asm block that writes M0 must save it first and put the saved value back as its last M0 write (the
+LDS-DMA copy takes M0 as an input operand and writes none).  A VMEM instruction that reads an SGPR
+needs 5 wait states after a VALU instruction wrote it (the copy's buffer descriptor comes from
+v_readfirstlane): every inline-asm LDS-DMA copy is checked for that, walking back from the copy
+over every path into it.  Each scan is checked on a planted case."""
 import os
 import re
 import shutil
@@ -154,6 +157,8 @@ def test_no_early_reads_of_asm_mfma_results(tmp_path):
     # every inline-asm block that writes M0 hands the compiler's value back
     m0 = m0_unrestored(text)
     assert not m0, "inline asm leaves M0 changed: " + "; ".join(m0[:10])
+    sg = sgpr_vmem_hazards(text)
+    assert not sg, "\n".join(f"line {ln}: {ws} wait states: {ins}" for ln, ws, ins in sg[:20])
     late = late_operands(text)
     assert not late, "\n".join(f"{k} line {ln}: {ws} wait states: {ins}" for k, ln, ws, ins in late[:20])
 
@@ -188,6 +193,96 @@ def test_user_mod_kernels_pass_the_same_scans(tmp_path):
     for name, found in (("early", early_touches(text)), ("late", late_operands(text))):
         assert not found, name + "\n" + "\n".join(f"{k} line {ln}: {ws}: {ins}" for k, ln, ws, ins in found[:20])
     assert not m0_unrestored(text)
+    assert not sgpr_vmem_hazards(text)
+
+
+def _sgprs(tok):
+    m = re.match(r"s\[(\d+):(\d+)\]$", tok)
+    if m:
+        return set(range(int(m.group(1)), int(m.group(2)) + 1))
+    m = re.match(r"s(\d+)$", tok)
+    return {int(m.group(1))} if m else set()
+
+
+def sgpr_vmem_hazards(asm_text, need=5):
+    """(line, wait states, instructions) for inline-asm LDS-DMA copies (`buffer_load_* ... lds`)
+    whose descriptor SGPRs a VALU instruction wrote fewer than `need` wait states before.  The
+    walk goes back from the copy over every path that reaches it: at a label it continues into
+    the fall-through predecessor (unless that ends in an unconditional branch) and into every
+    branch to the label."""
+    lines = [l.strip() for l in asm_text.split("\n")]
+    labels, branches_to = {}, {}
+    for k, t in enumerate(lines):
+        if re.match(r"^[.\w$]+:", t) and not t.startswith(";"):
+            labels[t.split(":")[0]] = k
+        m = re.match(r"^s_c?branch\w*\s+(\S+)", t)
+        if m:
+            branches_to.setdefault(m.group(1), []).append(k)
+
+    def is_instr(t):
+        return t and not t.startswith(";") and not t.startswith(".") and not re.match(r"^[\w$]+:", t)
+
+    def walk(j, ws, regs, seen):
+        """hazards on the paths that end just before line j with ws wait states so far"""
+        found = []
+        while j >= 0 and ws < need:
+            t = lines[j]
+            if re.match(r"^[.\w$]+:", t) and not t.startswith(";"):
+                name = t.split(":")[0]
+                for b in branches_to.get(name, []):
+                    if (b, ws) not in seen:
+                        seen.add((b, ws))
+                        found += walk(b, ws, regs, seen)
+                k = j - 1  # fall-through predecessor: the last instruction before the label
+                while k >= 0 and not is_instr(lines[k]) and not re.match(r"^[.\w$]+:", lines[k]):
+                    k -= 1
+                if k < 0 or lines[k].startswith(("s_branch", "s_endpgm", "s_setpc")):
+                    return found
+                j -= 1
+                continue
+            j -= 1
+            if not is_instr(t):
+                continue
+            op = t.split()[0]
+            if op.startswith("v_") and len(t.split()) > 1 and _sgprs(t.split(None, 1)[1].split(",")[0]) & regs:
+                return found + [(ws, t)]
+            ws += int(t.split()[1]) + 1 if op == "s_nop" else 1
+        return found
+
+    out, in_asm = [], False
+    for i, t in enumerate(lines):
+        if t.startswith(";;#ASMSTART"):
+            in_asm = True
+            continue
+        if t.startswith(";;#ASMEND"):
+            in_asm = False
+            continue
+        if not (in_asm and t.startswith("buffer_load") and t.endswith(" lds")):
+            continue
+        regs = _sgprs(t.split(None, 1)[1].split(",")[1].strip())
+        for ws, u in walk(i - 1, 0, regs, set()):
+            out.append((i + 1, ws, u + "  ->  " + t))
+    return out
+
+
+def test_sgpr_vmem_scan_finds_planted_case():
+    good = ("\tv_readfirstlane_b32 s12, v48\n\ts_mov_b32 m0, s9\n\t;;#ASMSTART\n\ts_nop 4\n"
+            "\tbuffer_load_dwordx4 v192, s[12:15], 0 offen lds\n\t;;#ASMEND\n")
+    assert sgpr_vmem_hazards(good) == []
+    bad = good.replace("s_nop 4", "s_nop 1")
+    found = sgpr_vmem_hazards(bad)
+    assert [(ws, ins.split()[1]) for _, ws, ins in found] == [(3, "s12,")]
+    # a write of an SGPR the copy does not read is no hazard
+    assert sgpr_vmem_hazards(bad.replace("s12, v48", "s20, v48")) == []
+    # across a label: found through a branch to it (the write sits before the branch), and
+    # through the fall-through edge; not through a fall-through edge cut by s_branch
+    tail = bad.split("\n", 1)[1]
+    via_branch = "\tv_readfirstlane_b32 s13, v1\n\ts_cbranch_scc1 .LBB0_3\n\ts_nop 7\n\ts_branch .LBB0_9\n.LBB0_3:\n" + tail
+    assert [ws for _, ws, _ in sgpr_vmem_hazards(via_branch)] == [4]
+    fall = "\tv_readfirstlane_b32 s13, v1\n.LBB0_3:\n" + tail
+    assert [ws for _, ws, _ in sgpr_vmem_hazards(fall)] == [3]
+    cut = "\tv_readfirstlane_b32 s13, v1\n\ts_branch .LBB0_9\n.LBB0_3:\n" + tail
+    assert sgpr_vmem_hazards(cut) == []
 
 
 def m0_unrestored(asm_text):
