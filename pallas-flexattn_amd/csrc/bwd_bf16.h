@@ -556,7 +556,7 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   // exponential's stage.  sched_barrier fences keep
   // the compiler to this order.
   auto tile_fast = [&](int qbase, int hq, float slope, const char* ql, const char* dl_, const float* lsel,
-                       const float* dltl, auto&& copy_k, auto&& stat_k, auto masked_c) {
+                       const float* dltl, auto&& prep, auto&& copy_k, auto&& stat_k, auto masked_c) {
     constexpr bool kMasked = decltype(masked_c)::value;
     constexpr int KS = KSTEPS, NSTEP = 4 * KS, PF = APF, R = PF + 1;
     static_assert(NDMA + 1 < NSTEP, "the next tile's copies fit the steps before its LSE store");
@@ -701,6 +701,10 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
     };
 #pragma unroll
     for (int t = 0; t < PF; ++t) load(t);
+    // the next tile's walk and copy plan (scalar work) while the first
+    // operand reads are in flight
+    __builtin_amdgcn_sched_barrier(0);
+    prep();
 #pragma unroll
     for (int t = 0; t < NSTEP; ++t) {
       const int ph = t / KS, s = t % KS;
@@ -766,14 +770,19 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   auto step = [&](int it, auto masked_c, auto buf_c) {
     constexpr int buf = decltype(buf_c)::value;  // == it & 1, a constant (immediate LDS offsets)
     const int hq = hq_next, qbase = qb_next;
-    // past the last tile the copies target qb = Sq (zeros into the idle buffer)
-    if (it + 1 < n_it) {
-      hq_next = ref_next.hq;
-      qb_next = walk.qbase(ref_next);
-    } else {
-      qb_next = P.Sq;
-    }
-    const TileCopy next = plan(hq_next, qb_next, buf ^ 1);
+    // the next tile and its copies (past the last tile they target qb = Sq:
+    // zeros into the idle buffer); run by tile_fast once its first LDS reads
+    // are issued
+    TileCopy next;
+    auto prep = [&]() {
+      if (it + 1 < n_it) {
+        hq_next = ref_next.hq;
+        qb_next = walk.qbase(ref_next);
+      } else {
+        qb_next = P.Sq;
+      }
+      next = plan(hq_next, qb_next, buf ^ 1);
+    };
     auto copy_k = [&](int k) { copy_part(next, k); };
     auto stat_k = [&]() { stat_store(next); };
     auto fetch_next = [&]() { ref_next = walk.fetch(min(it + 2, n_it - 1)); };
@@ -781,9 +790,11 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
       const float slope = (kMods && P.alibi) ? P.alibi[hq] : 0.f;
       tile_fast(qbase, hq, slope, lds + buf * TILE, lds + (2 + buf) * TILE,
                 reinterpret_cast<const float*>(lds + 4 * TILE + buf * STAT),
-                reinterpret_cast<const float*>(lds + 4 * TILE + (2 + buf) * STAT), copy_k, stat_k, masked_c);
+                reinterpret_cast<const float*>(lds + 4 * TILE + (2 + buf) * STAT), prep, copy_k, stat_k,
+                masked_c);
       fetch_next();
     } else {
+      prep();
 #pragma unroll
       for (int k = 0; k < NDMA; ++k) copy_k(k);
       fetch_next();
