@@ -6,9 +6,10 @@ The headline workload (default ns) is causal attention B4 H32 S8192 D128 in
 bf16, the shape the 50 % / 35 % targets are set on; the other workloads
 (C2 causal S2048, C3 sliding window, C4 GQA + ALiBi + soft-cap, C5 packed
 documents) are timed after it and reported as extra keys.
-A step is one forward + backward pass (fa_fwd, fa_bwd_preprocess,
-fa_bwd_dkdv, fa_bwd_dq through the C ABI, outputs preallocated, inputs
-resident in HBM) over one batch of synthetic inputs.  Throughput counts only
+A step is one forward + backward pass (fa_fwd and fa_bwd through the C ABI,
+outputs preallocated, inputs resident in HBM) over one batch of synthetic
+inputs; for these bf16 workloads fa_bwd is two launches (the dQ kernel, which
+also computes Delta = rowsum(O dO), then dK/dV).  Throughput counts only
 unmasked (query, key) pairs P per (batch, head): fwd 4*D*P, bwd 10*D*P,
 fwd+bwd 14*D*P FLOPs (recomputation is not credited).
 
@@ -363,9 +364,12 @@ def main():
     torch.cuda.synchronize()
     log(f"timed {args.steps} steps: {ms_step:.3f} ms/step")
 
+    # per-kernel times: the forward, the whole backward, and the staged
+    # kernels (Delta pass, dK/dV, dQ reading Delta); the dQ kernel with
+    # Delta fused takes about bwd - bwd_dkdv
     kernels = {}
-    for name, fn in (("fwd", runner.fwd), ("bwd_preprocess", runner.preprocess), ("bwd_dkdv", runner.dkdv),
-                     ("bwd_dq", runner.dq_)):
+    for name, fn in (("fwd", runner.fwd), ("bwd", runner.bwd), ("bwd_preprocess", runner.preprocess),
+                     ("bwd_dkdv", runner.dkdv), ("bwd_dq", runner.dq_)):
         fn()
         kernels[name] = time_region(fn, args.steps, stream)
     ms_fwd = kernels["fwd"]

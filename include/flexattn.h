@@ -54,7 +54,7 @@ enum fa_status {
   FA_ERR_TABLES = -5,        /* block tables inconsistent with the sizes */
   FA_ERR_WORKSPACE = -6,     /* workspace missing or too small */
   FA_ERR_LAUNCH = -7,        /* the HIP launch failed */
-  FA_ERR_VERSION = -8,       /* params.abi_version != FA_ABI_VERSION */
+  FA_ERR_VERSION = -8,       /* params.abi_version != FA_ABI_VERSION, or a mods blob of another build */
   FA_ERR_TOO_LARGE = -9,     /* beyond the fixed scratch of fa_bwd_noalloc */
   FA_ERR_COMPILE = -10       /* the run-time compile of user mods failed (see its log) */
 };
@@ -158,7 +158,9 @@ int fa_fwd_kvcache(const fa_params *p, const fa_kv_cache *kv, const void *q, con
  * keys past Skv finite (zero, as fa_quantize_fp8 writes them).  Every 128-row
  * block of a head (queries for Q, keys for K and V) carries one float scale,
  * a power of two in [2^-126, 2^127]: the tensor's value is element x scale.
- * Scales are (B * Hq, ceil(Sq / 128)) for Q, (B * Hkv, ceil(Skv / 128)) for K
+ * The kernel reads only a scale's exponent field (the E8M0 scale operand of
+ * the MFMA): other scale values are undefined behaviour, not checked here
+ * (the Python binding checks them).  Scales are (B * Hq, ceil(Sq / 128)) for Q, (B * Hkv, ceil(Skv / 128)) for K
  * and V.  Both products run on the scaled fp8 MFMA (S exact in fp32; P
  * rounded to e4m3 as p * 8).  Masks, block tables and the built-in score mods
  * as fa_fwd's bf16 path (document labels only as contiguous runs); o is bf16,
@@ -202,7 +204,11 @@ size_t fa_bwd_workspace_bytes(const fa_params *p);
 
 /* Backward: gradients of sum(o * dout) w.r.t. q, k, v, given o and lse from fa_fwd.
  * dk / dv are written (not accumulated); with GQA they sum over the q heads
- * sharing each kv head. */
+ * sharing each kv head.  The workspace receives Delta = rowsum(o * dout)
+ * (fp32, B * Hq * Sq); on the bf16 tile kernels (window / contiguous-document
+ * masks) the dQ kernel computes it, bit-identical to fa_bwd_preprocess, and
+ * the call is two launches (dQ, then dK/dV) instead of the reference's three
+ * stages (flash_attn.py:410-461). */
 int fa_bwd(const fa_params *p, const void *q, const void *k, const void *v, const void *o,
            const float *lse, const void *dout, void *dq, void *dk, void *dv, void *workspace,
            size_t workspace_bytes, void *stream);
@@ -215,7 +221,11 @@ int fa_bwd(const fa_params *p, const void *q, const void *k, const void *v, cons
  * library's first use on a GPU until the process ends); problems with
  * B * Hq * Sq above that return FA_ERR_TOO_LARGE.  Same kernels and results
  * as fa_bwd.  Calls on one GPU share that array: calls that overlap in time
- * on the same GPU (different streams, or threads) race and must not be made. */
+ * on the same GPU (different streams, or threads) race and must not be made.
+ * The array's device address is looked up on a device's first launching call
+ * of any entry point (fa_fwd, fa_bwd*, fa_mods_*, fa_fwd_fp8), so a graph
+ * capture of fa_bwd_noalloc made after the forward has run eagerly performs
+ * no lookup or module load while capturing; it records no memset. */
 size_t fa_bwd_noalloc_max_rows(void);
 int fa_bwd_noalloc(const fa_params *p, const void *q, const void *k, const void *v, const void *o,
                    const float *lse, const void *dout, void *dq, void *dk, void *dv, void *stream);
@@ -241,6 +251,10 @@ int fa_bwd_noalloc(const fa_params *p, const void *q, const void *k, const void 
  * apply; the built-in ALiBi / soft-cap apply when kScore is false (flag
  * FA_MODS_BUILTIN_SCORE when they are set).
  *
+ * flags: FA_MODS_MASK iff kMask, FA_MODS_SCORE iff kScore (checked when
+ * compiling), FA_MODS_BUILTIN_SCORE only without FA_MODS_SCORE; a call whose
+ * params set alibi_slopes or softcap needs a blob with FA_MODS_BUILTIN_SCORE
+ * (FA_ERR_UNSUPPORTED otherwise).
  * fa_mods_compile (no GPU needed) returns a blob (malloc'd, release with
  * fa_mods_free_blob) holding the code object; fa_mods_load loads it on the
  * current GPU.  Kernel tiles are fixed: bf16 128 x 64 (forward, dQ) and
@@ -252,7 +266,13 @@ typedef struct fa_mods fa_mods;
 int fa_mods_compile(const char *policy_source, int dtype, int D, int flags, void **blob, size_t *blob_bytes,
                     char *log, size_t log_bytes);
 void fa_mods_free_blob(void *blob);
+/* Refuses (FA_ERR_VERSION, before any GPU call) a blob whose header names
+ * another ABI version, other kernel headers (fa_mods_source_hash) or other
+ * kernel argument sizes than this library's. */
 int fa_mods_load(const void *blob, size_t blob_bytes, fa_mods **out);
+/* Hash of the kernel headers embedded for run-time compiles: a key for
+ * caching blobs across processes (blobs from other headers do not load). */
+uint64_t fa_mods_source_hash(void);
 int fa_mods_unload(fa_mods *m);
 int fa_mods_fwd(const fa_mods *m, const fa_params *p, const void *const *bufs, int nbufs, const void *q,
                 const void *k, const void *v, void *o, float *lse, void *stream);

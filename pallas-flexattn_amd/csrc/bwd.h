@@ -34,7 +34,20 @@ struct BwdArgs {
   void* dk;
   void* dv;
   float* delta;  // workspace (B, Hq, Sq)
+  // bf16 dQ tile kernel only: compute Delta itself from O and dO and write it
+  // to `delta` (the whole backward then runs dQ before dK/dV, no Delta pass)
+  int fuse_delta;
 };
+
+// sum_j O[j] dO[j] over one 16-byte chunk of bf16 (8 elements), in the order
+// both Delta paths use (the Delta kernel and the dQ kernel's fused form give
+// bit-identical rows)
+__device__ __forceinline__ float chunk_dot_bf16(u32x4 o, u32x4 d) {
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc += bf16_lo(o[j]) * bf16_lo(d[j]) + bf16_hi(o[j]) * bf16_hi(d[j]);
+  return acc;
+}
 
 // ---------------------------------------------------------------- Delta ----
 template <typename T, int D>
@@ -49,8 +62,7 @@ __global__ __launch_bounds__(256) void delta_kernel(BwdArgs a, int nrows) {
   const u32x4 dv = ld16(static_cast<const T*>(a.dout) + (size_t)row * D + c * (16 / ES), ok);
   float acc = 0.f;
   if constexpr (ES == 2) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc += bf16_lo(ov[j]) * bf16_lo(dv[j]) + bf16_hi(ov[j]) * bf16_hi(dv[j]);
+    acc = chunk_dot_bf16(ov, dv);
   } else {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc += __uint_as_float(ov[j]) * __uint_as_float(dv[j]);

@@ -187,6 +187,8 @@ void dq_bf16_kernel(BwdArgs a) {
   const bool qvalid = qw < P.Sq;
 
   frag qf[KSTEPS], df[KSTEPS];
+  frag of[KSTEPS];  // O rows, only with a.fuse_delta
+  const bool fuse = a.fuse_delta != 0;
   {
     const i32x4 rq = make_rsrc(static_cast<const char*>(a.q) + (size_t)head * P.Sq * RB, (uint32_t)P.Sq * RB);
     const i32x4 rd = make_rsrc(static_cast<const char*>(a.dout) + (size_t)head * P.Sq * RB, (uint32_t)P.Sq * RB);
@@ -195,12 +197,17 @@ void dq_bf16_kernel(BwdArgs a) {
       qf[s] = buf_load16(rq, qw * RB + (2 * s + hh) * 16);
       df[s] = buf_load16(rd, qw * RB + (2 * s + hh) * 16);
     }
+    if (fuse) {
+      const i32x4 ro = make_rsrc(static_cast<const char*>(a.o) + (size_t)head * P.Sq * RB, (uint32_t)P.Sq * RB);
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) of[s] = buf_load16(ro, qw * RB + (2 * s + hh) * 16);
+    }
   }
   const size_t rowi = (size_t)head * P.Sq + qw;
   // a row with no live key (LSE = -inf) gets P = 0 everywhere, like rows past Sq
   const float lse_row = qvalid ? a.lse[rowi] : -INFINITY;
   const float lse2 = lse_row > -INFINITY ? lse_row * kLog2e : INFINITY;
-  const float dl = qvalid ? a.delta[rowi] : 0.f;
+  float dl = (!fuse && qvalid) ? a.delta[rowi] : 0.f;
   const float slope = P.alibi ? P.alibi[h] : 0.f;
   const float cap_inv = P.softcap > 0.f ? 1.0f / P.softcap : 0.f;
   // with mods a tile holds y with the log2-domain logit ea * y: the logit
@@ -362,6 +369,21 @@ void dq_bf16_kernel(BwdArgs a) {
   // complete on every path into the loop
   wait_vmem();
   __syncthreads();
+  if (fuse) {
+    // Delta = sum_d O dO of this lane's row (rows past Sq read as zero): the
+    // lane holds 16-byte chunks 2 s + hh; they are summed pairwise at chunk
+    // distances D/16, ..., 2 inside the lane and 1 across the lane pair, the
+    // order of the Delta kernel's shuffle tree, so the rows are bit-identical
+    float x[KSTEPS];
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) x[s] = chunk_dot_bf16(of[s], df[s]);
+#pragma unroll
+    for (int st = KSTEPS / 2; st >= 1; st >>= 1)
+#pragma unroll
+      for (int s = 0; s < st; ++s) x[s] = x[s] + x[s + st];
+    dl = pair_sum(x[0]);
+    if (qvalid && hh == 0) a.delta[rowi] = dl;
+  }
   // dO is kept negated (bf16 sign flips), so the dP^T MFMA accumulates -dP
   // onto its starting value: started from Delta it gives Delta - dP, and
   // dS = -P (Delta - dP) takes one multiply per element
@@ -502,7 +524,9 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
     i32x4 rq, rdo, rst;
     int buf;
   };
-  constexpr int NDMA = 2 * TileDma<D, BQ, NW>::IPW + 1;
+  constexpr int NST = BQ / 64;  // LSE / Delta values per lane and tile
+  static_assert(BQ == 64 || BQ == 128, "q tile of 64 or 128 rows");
+  constexpr int NDMA = 2 * TileDma<D, BQ, NW>::IPW + NST;
   const bool stat_delta = (w & (NW >= 4 ? 2 : 1)) != 0;
   const float stat_scale = stat_delta ? 1.0f : -kLog2e;
   auto plan = [&](int hq, int qb, int buf) {
@@ -515,18 +539,21 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
     c.buf = buf;
     return c;
   };
-  static_assert(BQ <= 64, "one LSE value per lane");
-  float stat_in = 0.f;
+  float stat_in[NST];
+#pragma unroll
+  for (int r = 0; r < NST; ++r) stat_in[r] = 0.f;
   auto copy_part = [&](const TileCopy& c, int k) {
     constexpr int IPW = TileDma<D, BQ, NW>::IPW;
     if (k < IPW) dma.one(c.rq, k, lds + c.buf * TILE, w);
     else if (k < 2 * IPW) dma.one(c.rdo, k - IPW, lds + (2 + c.buf) * TILE, w);
-    else stat_in = __builtin_bit_cast(float, raw_buffer_load_b32(c.rst, lane * 4, 0, 0));
+    else stat_in[k - 2 * IPW] = __builtin_bit_cast(float, raw_buffer_load_b32(c.rst, (64 * (k - 2 * IPW) + lane) * 4, 0, 0));
   };
   auto stat_store = [&](const TileCopy& c) {
     // lanes past BQ store into the unused rest of the landing zone
-    *reinterpret_cast<float*>(lds + 4 * TILE + ((stat_delta ? 2 : 0) + c.buf) * STAT + lane * 4) =
-        stat_in * stat_scale;
+#pragma unroll
+    for (int r = 0; r < NST; ++r)
+      *reinterpret_cast<float*>(lds + 4 * TILE + ((stat_delta ? 2 : 0) + c.buf) * STAT + (64 * r + lane) * 4) =
+          stat_in[r] * stat_scale;
   };
   auto issue = [&](int hq, int qb, int buf) {
     const TileCopy c = plan(hq, qb, buf);
@@ -545,31 +572,34 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   }
 
   // One q tile (full or partial, with or without score mods): a fixed
-  // sequence of 4*KS steps of two MFMAs each, in four phases
+  // sequence of 2*NQS*KS steps of two MFMAs each.  Its 32-row sub-tiles run
+  // in pairs (2u, 2u + 1), four phases per pair
   //   A0: S_0, dP_0  |  A1: S_1, dP_1  |  C0: dV^T, dK^T += (sub-tile 0)  |  C1
   // with the exponentials / dS of sub-tile 0 (E0) spread over A1's steps and
   // those of sub-tile 1 (E1) over C0's, so VALU work issues while the matrix
-  // core is busy.  Every step also fetches the LDS operands of the step PF
-  // ahead (across phase boundaries; row fragments in A, transposed ones in C)
-  // and the LSE quad due next (Delta is the dP MFMAs' initial value, read at
-  // the start).  Score mods, when present, are evaluated branch-free in the
-  // exponential's stage.  sched_barrier fences keep
-  // the compiler to this order.
+  // core is busy; the next pair's accumulators are set up during C1.  Every
+  // step also fetches the LDS operands of the step PF ahead (across phase and
+  // pair boundaries; row fragments in A, transposed ones in C) and the LSE
+  // quad due next (Delta is the dP MFMAs' initial value).  Score mods, when
+  // present, are evaluated branch-free in the exponential's stage.
+  // sched_barrier fences keep the compiler to this order.
   auto tile_fast = [&](int qbase, int hq, float slope, const char* ql, const char* dl_, const float* lsel,
                        const float* dltl, auto&& prep, auto&& copy_k, auto&& stat_k, auto masked_c) {
     constexpr bool kMasked = decltype(masked_c)::value;
-    constexpr int KS = KSTEPS, NSTEP = 4 * KS, PF = APF, R = PF + 1;
+    constexpr int KS = KSTEPS, NSTEP = 2 * NQS * KS, PF = APF, R = PF + 1;
     static_assert(NDMA + 1 < NSTEP, "the next tile's copies fit the steps before its LSE store");
-    static_assert(2 * DT == KS && NQS == 2, "fast path shape");
-    // Partial tiles: element e of sub-tile j is query qbase + 32 j + 8 hh +
-    // r(e), r(e) = acc_row(e, 0) < 24.  rmask[j] has bit r set iff that query
+    static_assert(2 * DT == KS && NQS % 2 == 0, "fast path shape");
+    // Partial tiles: element e of sub-tile J is query qbase + 32 J + 8 hh +
+    // r(e), r(e) = acc_row(e, 0) < 24.  rmask[J] has bit r set iff that query
     // sees this lane's key; the packed P and dS words are ANDed with the
     // matching 0 / 0xffff halves, so masked elements contribute exact zeros
     // whatever their exponential came out as.
-    uint32_t rmask[2] = {0u, 0u};
+    uint32_t rmask[NQS];
+#pragma unroll
+    for (int j = 0; j < NQS; ++j) rmask[j] = 0u;
     if constexpr (kMasked) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < NQS; ++j) {
         const int base = qbase + 32 * j + 8 * hh;
         const int lo = max(qlo - base, 0), hi = min(qhi - base, 31);
         const uint32_t up = 0xffffffffu >> (31 - max(hi, 0));
@@ -587,45 +617,49 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
       }
     }
     // 0xffff / 0 halves for the two elements of pair p (rows r, r + 1)
-    auto pair_mask = [&](int j, int p) {
+    auto pair_mask = [&](int J, int p) {
       const int r = acc_row(2 * p, 0);
-      const uint32_t lo = (uint32_t)__builtin_amdgcn_sbfe((int)rmask[j], r, 1);
-      const uint32_t hi = (uint32_t)__builtin_amdgcn_sbfe((int)rmask[j], r + 1, 1);
+      const uint32_t lo = (uint32_t)__builtin_amdgcn_sbfe((int)rmask[J], r, 1);
+      const uint32_t hi = (uint32_t)__builtin_amdgcn_sbfe((int)rmask[J], r + 1, 1);
       return (lo & 0xffffu) | (hi & 0xffff0000u);
     };
     // E work in pairs of elements, spread evenly over the KS steps of its
-    // phase (phase 1 for sub-tile 0, phase 2 for sub-tile 1): pair p at step
-    // p * KS / 8, the LSE quad it needs read one step earlier.
+    // phase (A1 for sub-tile 2u, C0 for 2u + 1): pair p at step p * KS / 8,
+    // the LSE quad it needs read one step earlier.
     auto pair_step = [](int p) { return p * KS / 8; };
+    // local accumulators of the current pair: sacc from zero, pacc from Delta
+    // (dP accumulates onto it: pacc = Delta - dP, V negated)
     f32x16 sacc[2], pacc[2];
-    zero(sacc[0]);
-    zero(sacc[1]);
-    // dP accumulates onto Delta: pacc = Delta - dP (V negated)
+    auto init_pair = [&](int u) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < 2; ++j) {
+        zero(sacc[j]);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const f32x4 d4 = *reinterpret_cast<const f32x4*>(dltl + 32 * j + acc_row(4 * q, hh));
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(dltl + 32 * (2 * u + j) + acc_row(4 * q, hh));
 #pragma unroll
-        for (int i = 0; i < 4; ++i) pacc[j][4 * q + i] = d4[i];
+          for (int i = 0; i < 4; ++i) pacc[j][4 * q + i] = d4[i];
+        }
       }
+    };
+    init_pair(0);
     frag pf[2][2], sf[2][2];
     frag ring[R][2];
     f32x4 ls[2][4];
     auto load = [&](int t) {
-      const int ph = t / KS, s = t % KS;
-      if (ph < 2) {
-        ring[t % R][0] = rt.a_frag(ql, ph, s);
-        ring[t % R][1] = rt.a_frag(dl_, ph, s);
+      const int ph = t / KS, s = t % KS, u = ph / 4, lph = ph % 4;
+      if (lph < 2) {
+        ring[t % R][0] = rt.a_frag(ql, 2 * u + lph, s);
+        ring[t % R][1] = rt.a_frag(dl_, 2 * u + lph, s);
       } else {
-        const int j = ph - 2;
-        ring[t % R][0] = rt.t_frag(dl_, s >> 1, 2 * j + (s & 1));
-        ring[t % R][1] = rt.t_frag(ql, s >> 1, 2 * j + (s & 1));
+        const int J = 2 * u + lph - 2;
+        ring[t % R][0] = rt.t_frag(dl_, s >> 1, 2 * J + (s & 1));
+        ring[t % R][1] = rt.t_frag(ql, s >> 1, 2 * J + (s & 1));
       }
     };
-    auto load_stats = [&](int j, int q) {
-      const int r0 = 32 * j + acc_row(4 * q, hh);
-      ls[j][q] = *reinterpret_cast<const f32x4*>(lsel + r0);
+    auto load_stats = [&](int J, int q) {
+      const int r0 = 32 * J + acc_row(4 * q, hh);
+      ls[J & 1][q] = *reinterpret_cast<const f32x4*>(lsel + r0);
     };
     // A pair's E work in two stages a step apart, so the exponentials'
     // latency passes under the next step's MFMAs: e_exp (P), then e_use (dS,
@@ -635,18 +669,21 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
     // built-in mods: the lane's ALiBi offset per sub-tile and the soft-cap constants
     // with the score's factor f (2 log2(e) / cap with the soft-cap, log2(e)
     // without) folded into the lane's ALiBi base, the slope and the scale
-    float asb[2] = {0.f, 0.f}, msl = 0.f, msc = 0.f, mea = 1.0f;
+    float asb[NQS], msl = 0.f, msc = 0.f, mea = 1.0f;
+#pragma unroll
+    for (int j = 0; j < NQS; ++j) asb[j] = 0.f;
     bool capped = false;
     if constexpr (kMods && !Mod::kScore) {
       capped = P.softcap > 0.f;
       const float f = capped ? 2.0f * kLog2e * cap_inv : kLog2e;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) asb[j] = f * slope * (float)(kw - (qbase + 32 * j + 8 * hh));
+      for (int j = 0; j < NQS; ++j) asb[j] = f * slope * (float)(kw - (qbase + 32 * j + 8 * hh));
       msl = -f * slope;
       msc = f * P.scale;
       mea = capped ? P.softcap * kLog2e : 1.0f;
     }
-    auto e_exp = [&](int j, int p) {
+    auto e_exp = [&](int J, int p) {
+      const int j = J & 1;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int e = 2 * p + i, q = e >> 2;
@@ -654,13 +691,13 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
           // built-in ALiBi + soft-cap (branch-free: both results, selected):
           // u = f (scale q.k + slope (k - q)); tanh(s / cap) = 1 - 2 / (2^u + 1)
           // as one exp2 and one rcp; the logit is cap log2(e) tanh, or u
-          const float u = fmaf(sacc[j][e], msc, fmaf(msl, (float)acc_row(e, 0), asb[j]));
+          const float u = fmaf(sacc[j][e], msc, fmaf(msl, (float)acc_row(e, 0), asb[J]));
           const float th = fmaf(-2.0f, fast_rcp(fast_exp2(u) + 1.0f), 1.0f);
           dsq[p][i] = capped ? fmaf(-th, th, 1.0f) : 1.0f;
           pvq[p][i] = fast_exp2(fmaf(mea, capped ? th : u, ls[j][q][e & 3]));
         } else if constexpr (kMods) {
           // score mods (log2-domain logit) and d s / d(scale q.k) for dS
-          const float t = mod_score_flat<Mod>(P, sacc[j][e], slope, b, hq, qbase + 32 * j + acc_row(e, hh), kw,
+          const float t = mod_score_flat<Mod>(P, sacc[j][e], slope, b, hq, qbase + 32 * J + acc_row(e, hh), kw,
                                               cap_inv, &dsq[p][i]);
           pvq[p][i] = fast_exp2(t + ls[j][q][e & 3]);
         } else {
@@ -668,7 +705,8 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
         }
       }
     };
-    auto e_use = [&](int j, int p) {
+    auto e_use = [&](int J, int p) {
+      const int j = J & 1;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int e = 2 * p + i;
@@ -689,7 +727,7 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
         if constexpr (kMasked) {
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
-            const uint32_t m = pair_mask(j, 4 * half + w);
+            const uint32_t m = pair_mask(J, 4 * half + w);
             pf[j][half][w] &= m;
             sf[j][half][w] &= m;
           }
@@ -707,33 +745,40 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
     prep();
 #pragma unroll
     for (int t = 0; t < NSTEP; ++t) {
-      const int ph = t / KS, s = t % KS;
+      const int ph = t / KS, s = t % KS, u = ph / 4, lph = ph % 4;
       if (t + PF < NSTEP) load(t + PF);
-      // LSE of the quads whose first pair comes in the next step
+      // LSE of the quads whose first pair comes in the next step (sub-tile J's
+      // E work runs in phase 4 (J / 2) + (J % 2) + 1)
 #pragma unroll
       for (int q = 0; q < 4; ++q)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          if ((j + 1) * KS + pair_step(2 * q) == t + 1) load_stats(j, q);
-      if (ph < 2) {
-        sacc[ph] = E::mma(ring[t % R][0], kf[s], sacc[ph]);
-        pacc[ph] = E::mma(ring[t % R][1], vf[s], pacc[ph]);
+        for (int J = 0; J < NQS; ++J)
+          if ((4 * (J >> 1) + (J & 1) + 1) * KS + pair_step(2 * q) == t + 1) load_stats(J, q);
+      if (lph < 2) {
+        sacc[lph] = E::mma(ring[t % R][0], kf[s], sacc[lph]);
+        pacc[lph] = E::mma(ring[t % R][1], vf[s], pacc[lph]);
       } else {
-        const int j = ph - 2;
+        const int j = lph - 2;
         // the packing fences P and dS (see e_use), so no s_nop here
         mfma_acc<'a', false>(dva[s >> 1], ring[t % R][0], pf[j][s & 1]);
         mfma_acc<'a', false>(dka[s >> 1], ring[t % R][1], sf[j][s & 1]);
       }
-      if (t > 0 && ((t - 1) / KS == 1 || (t - 1) / KS == 2)) {  // second stage of last step's pairs
+      if (t > 0) {  // second stage of last step's pairs
+        const int pph = (t - 1) / KS, plph = pph % 4;
+        if (plph == 1 || plph == 2) {
+#pragma unroll
+          for (int p = 0; p < 8; ++p)
+            if (pair_step(p) == (t - 1) % KS) e_use(2 * (pph / 4) + plph - 1, p);
+        }
+      }
+      if (lph == 1 || lph == 2) {
 #pragma unroll
         for (int p = 0; p < 8; ++p)
-          if (pair_step(p) == (t - 1) % KS) e_use((t - 1) / KS - 1, p);
+          if (pair_step(p) == s) e_exp(2 * u + lph - 1, p);
       }
-      if (ph == 1 || ph == 2) {
-#pragma unroll
-        for (int p = 0; p < 8; ++p)
-          if (pair_step(p) == s) e_exp(ph - 1, p);
-      }
+      // the next pair's accumulators, once sub-tile 2u + 1's E work is done
+      // (its last pair's second stage runs in C1's first step)
+      if (lph == 3 && s == 1 && 2 * u + 2 < NQS) init_pair(u + 1);
       // the next tile's copies, one per step; its LSE stored near the end
       if (t < NDMA) copy_k(t);
       if (t == NSTEP - 2) stat_k();

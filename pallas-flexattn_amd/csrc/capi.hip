@@ -33,6 +33,35 @@ using fa::launch_status;
 using fa::Problem;
 using fa::Tiles;
 
+// ------------------------------------------------ allocation-free bwd ----
+// fa_bwd_noalloc keeps its Delta rows (B * Hq * Sq floats) in this array
+// instead of a caller workspace: 32 MiB per GPU, held from the library's
+// first use on that GPU until the process ends.  In host code `scratch` is
+// only a handle: its device address on the current GPU comes from
+// hipGetSymbolAddress, taken once per device and kept in scratch_ptr.  Every
+// launching entry point resolves it on its first call on a device, so a
+// caller that captures fa_bwd_noalloc into a HIP graph has already resolved
+// it (with the forward, or any other launch, made before the capture).
+constexpr size_t kScratchFloats = size_t(8) << 20;
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+float* scratch_ptr[kMaxDevices] = {nullptr};
+
+// Device address of this device's scratch array (nullptr on failure).
+float* device_scratch() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+    scratch_ptr[dev] = static_cast<float*>(ptr);
+  }
+  return scratch_ptr[dev];
+}
+
 // The tiles of a call: the requested ones (0 = default) where an
 // instantiation exists.  bf16 interval kernels: (bm, bn) in {(128, 64),
 // (64, 64)} and, for D >= 64, {(128, 32), (128, 128), (256, 64)}; dK/dV key
@@ -170,11 +199,27 @@ int fwd_d(const FwdArgs& a, int D, const Tiles& t, hipStream_t s) {
 
 bool has_mods(const Problem& p) { return p.alibi != nullptr || p.softcap > 0.f; }
 
-enum { kStageDelta = 1, kStageDkdv = 2, kStageDq = 4 };
+enum { kStageDelta = 1, kStageDkdv = 2, kStageDq = 4, kStageAll = 7 };
+
+// dK/dV query tile of the bf16 interval kernels: 128 rows (measured at causal
+// B4 H32 S8192 D128: step 9.10-9.14 against 9.33-9.36 ms with 64-row tiles)
+#ifndef FA_DKDV_BQ
+#define FA_DKDV_BQ 128
+#endif
+constexpr bool kDkdvQ128 = FA_DKDV_BQ == 128;
 
 template <typename T, int D, bool M>
 int bwd_all(const BwdArgs& a, const Tiles& t, int stages, hipStream_t s) {
   int rc = FA_OK;
+  if (stages == kStageAll && sizeof(T) == 2 && interval_masks(a.p)) {
+    // the bf16 dQ tile kernel computes Delta from O and dO and writes it, so
+    // the whole backward is two launches: dQ, then dK/dV reading that Delta
+    BwdArgs f = a;
+    f.fuse_delta = 1;
+    rc = fa::launch_dq<T, D, M>(f, t, s);
+    if (!rc) rc = fa::launch_dkdv<T, D, M>(a, t, s);
+    return rc;
+  }
   if (stages & kStageDelta) rc = fa::launch_delta<T, D>(a, s);
   if (!rc && (stages & kStageDkdv)) rc = fa::launch_dkdv<T, D, M>(a, t, s);
   if (!rc && (stages & kStageDq)) rc = fa::launch_dq<T, D, M>(a, t, s);
@@ -193,6 +238,7 @@ int bwd_d(const BwdArgs& a, int D, const Tiles& t, int stages, hipStream_t s) {
 // Validates the params for the requested backward stages and launches them.
 int bwd_stages(const fa_params* p, BwdArgs& a, int stages, hipStream_t s) {
   if (!p) return FA_ERR_NULL;
+  (void)device_scratch();
   if (p->dtype == FA_DTYPE_FP8_E4M3) return FA_ERR_DTYPE;  // the fp8 path is forward-only
   Tiles t;
   int rc = default_tiles(p, &t);
@@ -205,6 +251,11 @@ int bwd_stages(const fa_params* p, BwdArgs& a, int stages, hipStream_t s) {
     if ((stages & kStageDq) && !a.p.kv_num && !a.p.full_kv_num) return FA_ERR_TABLES;
     if ((stages & kStageDkdv) && !a.p.q_num && !a.p.full_q_num) return FA_ERR_TABLES;
   }
+  // dK/dV of bf16 interval masks in 128-query tiles, where the q-side tables
+  // allow them (half the per-tile boundaries of 64-query tiles)
+  if (kDkdvQ128 && p->dtype == FA_DTYPE_BF16 && p->D >= 64 && t.bkv == 128 && interval_masks(a.p) &&
+      (!a.p.has_tables || a.p.mblk_q % 128 == 0))
+    t.bq = 128;
   const bool m = has_mods(a.p);
   if (p->dtype == FA_DTYPE_BF16)
     return m ? bwd_d<uint16_t, true>(a, p->D, t, stages, s) : bwd_d<uint16_t, false>(a, p->D, t, stages, s);
@@ -213,32 +264,6 @@ int bwd_stages(const fa_params* p, BwdArgs& a, int stages, hipStream_t s) {
 
 size_t delta_bytes(const fa_params* p) {
   return ((size_t)p->B * p->Hq * p->Sq * sizeof(float) + 255) & ~(size_t)255;
-}
-
-// ------------------------------------------------ allocation-free bwd ----
-// fa_bwd_noalloc keeps its Delta rows (B * Hq * Sq floats) in this array
-// instead of a caller workspace: 32 MiB per GPU, held from the library's
-// first use on that GPU until the process ends.  In host code `scratch` is
-// only a handle: its device address on the current GPU comes from
-// hipGetSymbolAddress, taken once per device and kept in scratch_ptr.
-constexpr size_t kScratchFloats = size_t(8) << 20;
-static __device__ __align__(256) float scratch[kScratchFloats];
-
-constexpr int kMaxDevices = 64;
-std::mutex scratch_mu;
-float* scratch_ptr[kMaxDevices] = {nullptr};
-
-// Device address of this device's scratch array (nullptr on failure).
-float* device_scratch() {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
-  std::lock_guard<std::mutex> lock(scratch_mu);
-  if (!scratch_ptr[dev]) {
-    void* ptr = nullptr;
-    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
-    scratch_ptr[dev] = static_cast<float*>(ptr);
-  }
-  return scratch_ptr[dev];
 }
 
 // ------------------------------------------------------ block masks ----
@@ -313,6 +338,7 @@ size_t split_bytes(const fa_params* p, int n) {
 int fwd_launch(const fa_params* p, const fa_kv_cache* kv, const void* q, const void* k, const void* v, void* o,
                float* lse, bool split, int n_splits, void* workspace, size_t workspace_bytes, void* stream) {
   if (!p) return FA_ERR_NULL;
+  (void)device_scratch();
   if (p->dtype == FA_DTYPE_FP8_E4M3) return FA_ERR_DTYPE;  // fa_fwd_fp8
   if (n_splits > 64) return FA_ERR_SHAPE;
   Tiles t;
@@ -364,6 +390,8 @@ extern "C" {
 
 int fa_abi_version(void) { return FA_ABI_VERSION; }
 
+uint64_t fa_mods_source_hash(void) { return kRtcHash; }
+
 const char* fa_strerror(int status) {
   switch (status) {
     case FA_OK: return "success";
@@ -374,7 +402,8 @@ const char* fa_strerror(int status) {
     case FA_ERR_TABLES: return "block tables inconsistent with the problem sizes";
     case FA_ERR_WORKSPACE: return "workspace missing or too small";
     case FA_ERR_LAUNCH: return "HIP kernel launch failed";
-    case FA_ERR_VERSION: return "fa_params.abi_version does not match the library";
+    case FA_ERR_VERSION:
+      return "ABI version mismatch: fa_params.abi_version, or a mods code blob built from other kernel headers";
     case FA_ERR_TOO_LARGE: return "B * Hq * Sq exceeds fa_bwd_noalloc_max_rows()";
     case FA_ERR_COMPILE: return "the run-time compile of the user mods failed (see the compile log)";
     default: return "unknown status";
@@ -401,6 +430,7 @@ int fa_fwd(const fa_params* p, const void* q, const void* k, const void* v, void
 
 int fa_fwd_fp8(const fa_params* p, const fa_fp8_inputs* in, void* o, float* lse, void* stream) {
   if (!p || !in) return FA_ERR_NULL;
+  (void)device_scratch();
   if (p->dtype != FA_DTYPE_FP8_E4M3) return FA_ERR_DTYPE;
   Tiles t;
   int rc = default_tiles(p, &t);
@@ -484,7 +514,7 @@ int fa_bwd(const fa_params* p, const void* q, const void* k, const void* v, cons
   a.dk = dk;
   a.dv = dv;
   a.delta = static_cast<float*>(workspace);
-  return bwd_stages(p, a, kStageDelta | kStageDkdv | kStageDq, static_cast<hipStream_t>(stream));
+  return bwd_stages(p, a, kStageAll, static_cast<hipStream_t>(stream));
 }
 
 size_t fa_bwd_noalloc_max_rows(void) { return kScratchFloats; }
@@ -509,8 +539,8 @@ int fa_bwd_noalloc(const fa_params* p, const void* q, const void* k, const void*
   a.dq = dq;
   a.dk = dk;
   a.dv = dv;
-  a.delta = delta;  // every row is written by the Delta kernel before it is read
-  return bwd_stages(p, a, kStageDelta | kStageDkdv | kStageDq, static_cast<hipStream_t>(stream));
+  a.delta = delta;  // every row is written (by the Delta pass or the dQ kernel) before it is read
+  return bwd_stages(p, a, kStageAll, static_cast<hipStream_t>(stream));
 }
 
 int fa_bwd_preprocess(const fa_params* p, const void* o, const void* dout, float* delta, void* stream) {

@@ -97,7 +97,7 @@ int run_dkdv(const BwdArgs& a, hipStream_t s) {
       return launch_status();
     }
   }
-  if constexpr (NW == 4) {
+  if constexpr (NW == 4 && BQ <= 64) {
     hipLaunchKernelGGL((fa::dkdv_kernel<T, D, BQ, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
     return launch_status();
   }
@@ -123,6 +123,9 @@ int launch_dkdv(const BwdArgs& a, const Tiles& t, hipStream_t s) {
   constexpr int BQ = sizeof(T) == 2 ? 64 : 32;
   if constexpr (sizeof(T) == 2 && D >= 64) {
     if (t.bkv == 64) return run_dkdv<T, D, BQ, 2, M>(a, s);
+    // 128-query tiles (bf16 tile kernel only: the C ABI picks them for
+    // interval masks and tables at a multiple of 128)
+    if (t.bq == 128) return run_dkdv<T, D, 128, 4, M>(a, s);
   }
   return run_dkdv<T, D, BQ, 4, M>(a, s);
 }

@@ -261,10 +261,10 @@ _HANDLES = {}
 
 
 def _lib_identity():
-    """Identifies the library build (the run-time compiled kernels come from
-    its embedded headers): size and modification time of the .so."""
-    st = os.stat(_lib.LIB_PATH)
-    return f"{st.st_size}-{int(st.st_mtime)}"
+    """Identifies the kernel headers the library compiles user mods from (a
+    blob built from other headers does not load): the ABI version and the
+    library's hash of its embedded headers."""
+    return f"abi{_lib.ABI_VERSION}-{_lib.load().fa_mods_source_hash():016x}"
 
 
 def _mods_handle(mods, dtype_code, D, flags, device):
@@ -590,6 +590,9 @@ class Runner:
         self.delta = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
         self.dq, self.dk, self.dv = torch.empty_like(self.q), torch.empty_like(self.k), torch.empty_like(self.v)
         self.lib = _lib.load()
+        # fa_bwd's workspace holds Delta (B, Hq, Sq) fp32
+        self.ws = torch.empty(max(self.lib.fa_bwd_workspace_bytes(self.plan.ptr()), 256), device=q.device,
+                              dtype=torch.uint8)
 
     def fwd(self):
         _lib.check(self.lib.fa_fwd(self.plan.ptr(), self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
@@ -609,12 +612,18 @@ class Runner:
                                       self.do.data_ptr(), self.lse.data_ptr(), self.delta.data_ptr(),
                                       self.dq.data_ptr(), _stream()))
 
+    def bwd(self):
+        """The whole backward (fa_bwd): for bf16 interval masks the dQ kernel
+        computes Delta, then dK/dV; otherwise Delta, dK/dV, dQ."""
+        _lib.check(self.lib.fa_bwd(self.plan.ptr(), self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
+                                   self.o.data_ptr(), self.lse.data_ptr(), self.do.data_ptr(), self.dq.data_ptr(),
+                                   self.dk.data_ptr(), self.dv.data_ptr(), self.ws.data_ptr(), self.ws.numel(),
+                                   _stream()))
+
     def step(self):
         """One forward + backward pass."""
         self.fwd()
-        self.preprocess()
-        self.dkdv()
-        self.dq_()
+        self.bwd()
 
 
 # ------------------------------------------------------------ public API ----
