@@ -77,7 +77,7 @@ EXPORTED = ("fa_fwd", "fa_fwd_fp8", "fa_quantize_fp8", "fa_fwd_host", "fa_bwd_pr
             "fa_bwd_noalloc", "fa_bwd_noalloc_max_rows", "fa_bwd_preprocess", "fa_bwd_dkdv", "fa_bwd_dq",
             "fa_mask_build_workspace_bytes", "fa_build_block_mask", "fa_strerror", "fa_abi_version",
             "fa_mods_compile", "fa_mods_free_blob", "fa_mods_load", "fa_mods_unload", "fa_mods_fwd", "fa_mods_bwd",
-            "fa_mods_bwd_dkdv", "fa_mods_bwd_dq")
+            "fa_mods_bwd_dkdv", "fa_mods_bwd_dq", "fa_mods_source_hash")
 
 MODS_MASK, MODS_SCORE, MODS_BUILTIN_SCORE = 1, 2, 4
 
@@ -163,6 +163,8 @@ def load():
     lib.fa_mods_bwd_dq.restype = i
     lib.fa_strerror.argtypes = [ctypes.c_int]
     lib.fa_strerror.restype = ctypes.c_char_p
+    lib.fa_mods_source_hash.argtypes = []
+    lib.fa_mods_source_hash.restype = ctypes.c_uint64
     lib.fa_abi_version.argtypes = []
     lib.fa_abi_version.restype = ctypes.c_int
     if lib.fa_abi_version() != ABI_VERSION:

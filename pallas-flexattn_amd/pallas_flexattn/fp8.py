@@ -54,7 +54,26 @@ def quantize_fp8(x, transpose: bool = False) -> Fp8Tensor:
     lib = _lib.load()
     _lib.check(lib.fa_quantize_fp8(x.data_ptr(), B * H, S, D, int(transpose), out.data_ptr(), scale.data_ptr(),
                                    _stream()))
+    scale._fa_scales_ok = scale._version  # powers of two in range by construction
     return Fp8Tensor(out, scale, S, bool(transpose))
+
+
+def _check_scales(t: Fp8Tensor, name: str) -> None:
+    """The kernels read a scale's exponent field only (it becomes the E8M0
+    scale operand of the MFMA): every scale must be a power of two 2^e with
+    e in [-126, 127].  A scale tensor carries the version it was checked at
+    (quantize_fp8's outputs are valid by construction), so the check (one
+    device sync) runs once per tensor and again after an in-place change."""
+    import torch
+    sc = t.scale
+    if getattr(sc, "_fa_scales_ok", None) == sc._version:
+        return
+    m, e = torch.frexp(sc)
+    ok = bool(((m == 0.5) & (e >= -125) & (e <= 128)).all())
+    if not ok:
+        raise ValueError(f"{name}: Fp8Tensor scales must be powers of two 2^e with -126 <= e <= 127 "
+                         "(the kernels use only their exponent)")
+    sc._fa_scales_ok = sc._version
 
 
 def dequantize_fp8(t: Fp8Tensor):
@@ -132,7 +151,8 @@ def _prepare(query, key, value, score_mod, block_mask, enable_gqa, resolve):
     mask, score, mods = resolve(mask_mod, score_mod)
     if mods is not None:
         raise NotImplementedError("the fp8 forward takes the built-in mask / score descriptors")
-    for t in (q8, k8, v8):
+    for t, name in ((q8, "query"), (k8, "key"), (v8, "value")):
         if not (t.data.is_contiguous() and t.scale.is_contiguous() and t.scale.dtype == torch.float32):
             raise ValueError("Fp8Tensor data and scales must be contiguous, scales float32")
+        _check_scales(t, name)
     return q8, k8, v8, mask, score, (B, Hq, Sq, D, Hkv, Skv)

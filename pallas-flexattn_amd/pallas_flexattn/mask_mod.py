@@ -6,8 +6,10 @@ the built-in ones are :class:`MaskSpec` descriptors, which are also callable
 with those two arguments (or PyTorch's ``(b, h, q_idx, kv_idx)``) on numpy
 arrays or torch tensors, and which the MI355X kernels evaluate natively as a
 fused epilogue: a window on ``delta = q - kv`` and/or equal document ids.
-Arbitrary callables still work with :func:`create_block_mask` and
-:func:`mha_reference`; the GPU kernels accept only descriptors.
+Arbitrary callables work everywhere too: :func:`create_block_mask` and
+:func:`mha_reference` evaluate them directly, and the GPU kernels run them
+after tracing (``lowering.py`` records the callable as an expression, which
+is compiled into the same tile kernels at run time).
 """
 from typing import Callable, Optional, Sequence, Union
 

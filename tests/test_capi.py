@@ -14,7 +14,7 @@ HEADER = os.path.join(ROOT, "include", "flexattn.h")
 
 def declared_functions():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|size_t|void|const char \*)\s*(fa_\w+)\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|uint64_t|void|const char \*)\s*(fa_\w+)\(", text, re.M)))
 
 
 def test_library_exports_every_declared_symbol():

@@ -164,3 +164,30 @@ def test_fp8_rejections():
     bm = pf.create_block_mask(pf.document_ids_mask(ids), 1, 2, 128, 128, 128)
     with pytest.raises(_lib.FlexAttnError):
         pf.flex_attention_fp8(x, x, x, block_mask=bm)
+
+
+def test_fp8_scales_must_be_powers_of_two():
+    """The kernel reads only the exponent field of each block scale, so the
+    binding refuses Fp8Tensor scales that are not powers of two in
+    [2^-126, 2^127] (not powers of two, zero, subnormal, negative, inf),
+    and accepts them again once fixed (the check follows in-place changes)."""
+    import torch
+    import pallas_flexattn as pf
+    from pallas_flexattn.fp8 import Fp8Tensor
+    print("[gpu fp8] scale validation", flush=True)
+    x = torch.randn(1, 2, 256, 64, device="cuda", dtype=torch.bfloat16)
+    q8, k8, v8 = pf.quantize_fp8(x), pf.quantize_fp8(x), pf.quantize_fp8(x, transpose=True)
+    pf.flex_attention_fp8(q8, k8, v8)
+    for bad in (0.75, 0.0, 2.0 ** -130, -1.0, float("inf")):
+        sc = k8.scale.clone()
+        sc[0, 1, 1] = bad
+        with pytest.raises(ValueError, match="powers of two"):
+            pf.flex_attention_fp8(q8, Fp8Tensor(k8.data, sc, k8.seq_len, False), v8)
+    sc = k8.scale.clone()
+    sc[0, 0, 0] = 3.0
+    kb = Fp8Tensor(k8.data, sc, k8.seq_len, False)
+    with pytest.raises(ValueError, match="powers of two"):
+        pf.flex_attention_fp8(q8, kb, v8)
+    sc[0, 0, 0] = 4.0  # fixed in place: checked again, accepted
+    pf.flex_attention_fp8(q8, kb, v8)
+    torch.cuda.synchronize()

@@ -165,3 +165,38 @@ def test_callable_mask_with_builtin_score_and_document_labels():
                                                                             np.full_like(s, 0.75)))
     for nm, got, want in (("O", o, wo), ("dQ", tq.grad, wdq), ("dK", tk.grad, wdk), ("dV", tv.grad, wdv)):
         assert_close(f"docs+score {nm}", to_np(got), want, BF16_TOL)
+
+
+def test_builtin_score_params_need_a_blob_built_for_them():
+    """A call whose params carry ALiBi slopes or a soft-cap runs the built-in
+    score epilogue only in a blob compiled with FA_MODS_BUILTIN_SCORE; a
+    mask-only blob refuses such params (FA_ERR_UNSUPPORTED) instead of
+    silently dropping them, before any launch."""
+    import ctypes
+    import torch
+    from pallas_flexattn import _lib, lowering as L
+    from pallas_flexattn.flash_attn import _Plan, _as_score_spec, _stream
+    pf = _pf()
+    print("[gpu user mods] builtin-score params with a mask-only blob", flush=True)
+    lib = _lib.load()
+    B, H, S, D = 1, 2, 128, 64
+    q, k, v = (torch.randn(B, H, S, D, device="cuda").to(torch.bfloat16) for _ in range(3))
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, S, device="cuda", dtype=torch.float32)
+    mods = L.UserMods(L.lower_mask(lambda qi, kv: (qi - kv) % 3 != 1), None)
+    blob = _lib.compile_mods(mods.source, _lib.DTYPE_BF16, D, mods.flags(False))
+    h = ctypes.c_void_p()
+    _lib.check(lib.fa_mods_load(blob, len(blob), ctypes.byref(h)))
+    try:
+        bufs = (ctypes.c_void_p * 1)()
+        for score in (pf.alibi_score_mod(H), pf.softcap_score_mod(20.0)):
+            plan = _Plan(q, k, None, _as_score_spec(score), None, None, (128, 64, 128))
+            rc = lib.fa_mods_fwd(h, plan.ptr(), bufs, 0, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                 lse.data_ptr(), _stream())
+            assert rc == -4, rc  # FA_ERR_UNSUPPORTED
+        plan = _Plan(q, k, None, None, None, None, (128, 64, 128))  # no built-in score: runs
+        _lib.check(lib.fa_mods_fwd(h, plan.ptr(), bufs, 0, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                   lse.data_ptr(), _stream()))
+        torch.cuda.synchronize()
+    finally:
+        _lib.check(lib.fa_mods_unload(h))

@@ -127,3 +127,54 @@ def test_policy_compiles_for_gfx950_without_a_gpu():
         assert len(blob) > 1000
     with pytest.raises(_lib.FlexAttnError, match="compiling the user mods failed"):
         _lib.compile_mods("struct UserMod { this is not C++ };", _lib.DTYPE_BF16, 64, 1)
+
+
+def test_policy_must_match_its_flags():
+    """fa_mods_compile refuses a policy whose kMask / kScore disagree with the
+    flags it is compiled under (the launches set up the mask walk and the
+    score epilogue from the flags), and a user score together with the
+    built-in ALiBi / soft-cap (which only run without a user score)."""
+    from pallas_flexattn import _lib
+    mods = L.UserMods(L.lower_mask(MASKS["parity"]), None)
+    assert mods.flags(False) == _lib.MODS_MASK
+    with pytest.raises(_lib.FlexAttnError, match="kMask disagrees"):
+        _lib.compile_mods(mods.source, _lib.DTYPE_BF16, 64, 0)
+    with pytest.raises(_lib.FlexAttnError, match="kScore disagrees"):
+        _lib.compile_mods(mods.source, _lib.DTYPE_BF16, 64, _lib.MODS_MASK | _lib.MODS_SCORE)
+    smods = L.UserMods(None, L.lower_score(lambda s, b, h, q, kv: s * 0.5))
+    with pytest.raises(_lib.FlexAttnError, match="exit 3"):
+        _lib.compile_mods(smods.source, _lib.DTYPE_BF16, 64, _lib.MODS_SCORE | _lib.MODS_BUILTIN_SCORE)
+
+
+def test_blob_from_other_kernel_headers_is_refused():
+    """A code blob records the ABI version, the hash of the kernel headers it
+    was compiled from and the kernel argument sizes; fa_mods_load refuses a
+    blob that differs in any of them (FA_ERR_VERSION) before any GPU call,
+    so a stale cached or stored blob is never launched with another argument
+    layout.  Header layout: magic u32, abi_version u32, header hash u64,
+    sizeof(FwdArgs) u32, sizeof(BwdArgs) u32."""
+    import ctypes
+    from pallas_flexattn import _lib
+    lib = _lib.load()
+    mods = L.UserMods(L.lower_mask(MASKS["parity"]), None)
+    blob = _lib.compile_mods(mods.source, _lib.DTYPE_BF16, 64, mods.flags(False))
+    assert int.from_bytes(blob[4:8], "little") == _lib.ABI_VERSION
+    assert int.from_bytes(blob[8:16], "little") == lib.fa_mods_source_hash()
+    fwd_bytes, bwd_bytes = int.from_bytes(blob[16:20], "little"), int.from_bytes(blob[20:24], "little")
+    assert 0 < fwd_bytes < 4096 and bwd_bytes > fwd_bytes - 512
+
+    def load(b):
+        h = ctypes.c_void_p()
+        return lib.fa_mods_load(bytes(b), len(b), ctypes.byref(h))
+
+    FA_ERR_SHAPE, FA_ERR_VERSION = -2, -8
+    for lo, hi, delta in ((4, 8, 1), (8, 16, 1), (16, 20, 8), (20, 24, 8)):
+        bad = bytearray(blob)
+        bad[lo:hi] = ((int.from_bytes(blob[lo:hi], "little") + delta) % (1 << (8 * (hi - lo)))).to_bytes(
+            hi - lo, "little")
+        assert load(bad) == FA_ERR_VERSION, (lo, hi)
+    bad = bytearray(blob)
+    bad[0] ^= 1  # not a blob
+    assert load(bad) == FA_ERR_SHAPE
+    assert load(blob[:-1]) == FA_ERR_SHAPE  # truncated code object
+    assert load(blob[:20]) == FA_ERR_SHAPE  # shorter than the header
