@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 2
+#define FA_ABI_VERSION 3
 
 enum fa_dtype {
   FA_DTYPE_BF16 = 0,
@@ -113,6 +113,15 @@ typedef struct fa_params {
   int32_t kv_width, q_width;
   const int32_t *kv_num_blocks, *kv_indices, *full_kv_num_blocks, *full_kv_indices;
   const int32_t *q_num_blocks, *q_indices, *full_q_num_blocks, *full_q_indices;
+  /* More kernel choices, 0 = library default (the reference's num_stages /
+   * block_r knobs become these gfx950 axes):
+   * block_q: queries per dK/dV q tile, bf16 only: 128 (the default where the
+   *   call allows it: D >= 64, block_kv 128, window / contiguous-document
+   *   masks, q-side tables at a multiple of 128) or 64 (every call).
+   * lds_stages: K / V tiles the bf16 forward holds in LDS at once: 2
+   *   (default), 3 with block_n 32 (copies two tiles ahead), 1 with block_n
+   *   128 (single buffer, twice the workgroups per CU). */
+  int32_t block_q, lds_stages;
 } fa_params;
 
 /* Forward: o = softmax(mask(score_mod(scale q k^T))) v, lse = logsumexp of the row. */

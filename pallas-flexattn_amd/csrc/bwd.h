@@ -72,111 +72,7 @@ __global__ __launch_bounds__(256) void delta_kernel(BwdArgs a, int nrows) {
   if (ok && c == 0) a.delta[row] = acc;
 }
 
-// q-tile walk of the dK/dV kernel over the q-side tables of all q heads in a group
-struct QWalk {
-  const Problem* P;
-  int b, hq0, g, kvrow, sub, bq, ntiles_dense;
-  bool dense;
-  int n_full, n_all;  // set by init()
-  // lists of the first head (all heads when the tables do not depend on the head)
-  int nf0, np0;
-  const int *fl0, *pl0;
-  __device__ __forceinline__ void head_lists(int hq, int* nf, const int** fl, int* np, const int** pl) const {
-    const int row = tab_row(*P, b, hq, kvrow, P->n_kvblk);
-    *nf = P->full_q_num ? clamp_count(scalar_load(P->full_q_num, row), P->q_width) : 0;
-    *fl = P->full_q_num ? P->full_q_idx + (size_t)row * P->q_width : nullptr;
-    *np = P->q_num ? clamp_count(scalar_load(P->q_num, row), P->q_width) : 0;
-    *pl = P->q_num ? P->q_idx + (size_t)row * P->q_width : nullptr;
-  }
-  // tiles of head hq in the full (part = 0) or partial (part = 1) list
-  __device__ __forceinline__ int per_head(int hq, int part) const {
-    if (dense) return (part == (P->has_mask ? 1 : 0)) ? ntiles_dense : 0;
-    int nf, np;
-    const int *fl, *pl;
-    head_lists(hq, &nf, &fl, &np, &pl);
-    return (part ? np : nf) * sub;
-  }
-  __device__ __forceinline__ int count_part(int part) const {
-    if (dense || P->tab_h == 1) return g * per_head(hq0, part);
-    int n = 0;
-    for (int i = 0; i < g; ++i) n += per_head(hq0 + i, part);
-    return n;
-  }
-  // Iteration order: the full tiles of every head of the group, then the
-  // partial ones, so a kernel can run the two kinds in separate loops.
-  __device__ __forceinline__ void init() {
-    n_full = count_part(0);
-    n_all = n_full + count_part(1);
-    nf0 = np0 = 0;
-    fl0 = pl0 = nullptr;
-    if (!dense) head_lists(hq0, &nf0, &fl0, &np0, &pl0);
-  }
-  __device__ __forceinline__ int count() const { return n_all; }
-  __device__ __forceinline__ int count_full() const { return n_full; }
-  // Table lookups stay off the scalar cache for the common layouts (one head,
-  // or tables shared by all heads): counts come from init(), the entry
-  // through a vector load that the caller consumes a tile later.
-  __device__ __forceinline__ TileRef fetch(int it) const {
-    const int part = it >= n_full ? 1 : 0;
-    int gi = 0, rem = part ? it - n_full : it;
-    int nf = nf0, np = np0;
-    const int *fl = fl0, *pl = pl0;
-    if (dense || P->tab_h == 1) {
-      if (g > 1) {
-        const int c = dense ? per_head(hq0, part) : (part ? np0 : nf0) * sub;
-        gi = c > 0 ? rem / c : 0;
-        rem -= gi * c;
-      }
-    } else {
-      for (; gi < g - 1; ++gi) {
-        const int c = per_head(hq0 + gi, part);
-        if (rem < c) break;
-        rem -= c;
-      }
-      if (gi > 0) head_lists(hq0 + gi, &nf, &fl, &np, &pl);
-    }
-    TileRef r{rem, 0, hq0 + gi};
-    if (!dense) {
-      const int bi = div_pow2_or(rem, sub, log2_if_pow2(sub));
-      r.s = rem - bi * sub;
-      r.raw = part ? vload_i32(pl, bi, np) : vload_i32(fl, bi, nf);
-    }
-    return r;
-  }
-  __device__ __forceinline__ int qbase(const TileRef& r) const {
-    if (dense) return r.raw * bq;
-    const int raw = __builtin_amdgcn_readfirstlane(r.raw);
-    return (raw < 0 || raw >= P->n_qblk) ? kPastEnd : raw * P->mblk_q + r.s * bq;
-  }
-  // -> q head, first query of the tile, whether the element mask applies
-  __device__ __forceinline__ void get(int it, int* hq, int* qbase, bool* masked) const {
-    const int part = it >= n_full ? 1 : 0;
-    int gi = 0, rem = part ? it - n_full : it;
-    if (dense || P->tab_h == 1) {
-      const int c = per_head(hq0, part);
-      gi = c > 0 ? rem / c : 0;
-      rem -= gi * c;
-    } else {
-      for (; gi < g - 1; ++gi) {
-        const int c = per_head(hq0 + gi, part);
-        if (rem < c) break;
-        rem -= c;
-      }
-    }
-    *hq = hq0 + gi;
-    *masked = part != 0;
-    if (dense) {
-      *qbase = rem * bq;
-      return;
-    }
-    int nf, np;
-    const int *fl, *pl;
-    head_lists(*hq, &nf, &fl, &np, &pl);
-    const int bi = rem / sub, s = rem - bi * sub;
-    const int idx = part ? scalar_load(pl, bi) : scalar_load(fl, bi);
-    *qbase = (idx < 0 || idx >= P->n_qblk) ? kPastEnd : idx * P->mblk_q + s * bq;
-  }
-};
+using QWalk = QWalkT<DeviceLoad>;
 
 // ----------------------------------------------------------------- dK dV ---
 template <typename T, int D, int BQ, int NW, bool kMods, class Mod = BuiltinMod>

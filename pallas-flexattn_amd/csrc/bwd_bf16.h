@@ -33,34 +33,12 @@
 namespace fa {
 
 // Lane-constant LDS offsets for reading a swizzled row-major bf16 tile
-// (chunk c of row r in slot c ^ chunk_swz(r)).
+// (chunk c of row r in slot c ^ chunk_swz(r); offsets from index.h).
 template <int D>
-struct RowTile {
-  static constexpr int RB = D * 2;
-  static constexpr int KCH = D / 8;
-  static constexpr int KSTEPS = D / 16;
-  static constexpr int DT = D / 32;
-  __device__ static __forceinline__ int swz(int r) { return chunk_swz<KCH>(r); }
-
-  int aoff[KSTEPS];  // A operand, rows perm23(lane%32) (+32j), k step s
-  int tr[2][DT];     // transposing read: [rows +0..3 / +4..7][d tile]
-
-  __device__ __forceinline__ void init(int lane) {
-    const int lr = lane & 31, hh = lane >> 5;
-    const int r = perm23(lr);
-#pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) aoff[s] = r * RB + (((2 * s + hh) ^ swz(r)) * 16);
-    const int s16 = lane & 15, g = lane >> 4;
-    const int rowbase = 8 * (g >> 1) + (s16 >> 2);
-    const int x = 2 * (g & 1) + ((s16 & 3) >> 1);
-#pragma unroll
-    for (int rd = 0; rd < 2; ++rd)
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const int row = 4 * rd + rowbase;
-        tr[rd][dt] = row * RB + (((4 * dt + x) ^ swz(row)) * 16) + (s16 & 1) * 8;
-      }
-  }
+struct RowTile : RowTileOffsets<D> {
+  using RowTileOffsets<D>::RB;
+  using RowTileOffsets<D>::aoff;
+  using RowTileOffsets<D>::tr;
   // A operand: rows 32*j + perm23(lane%32), d = 16*s + 8*(lane/32) + [0..7]
   __device__ __forceinline__ u32x4 a_frag(const char* tile, int j, int s) const {
     return *reinterpret_cast<const u32x4*>(tile + j * 32 * RB + aoff[s]);
@@ -78,23 +56,18 @@ struct RowTile {
 template <int D, int R, int NW>
 struct TileDma {
   static constexpr int RB = D * 2;
-  static constexpr int KCH = D / 8;
   static constexpr int IPW = R * RB / 1024 / NW;
   static_assert((R * RB) % (1024 * NW) == 0, "DMA split");
   int off[IPW];
   __device__ __forceinline__ void init(int lane, int w) {
 #pragma unroll
-    for (int u = 0; u < IPW; ++u) {
-      const int g = (w * IPW + u) * 64 + lane;
-      const int r = g / KCH, p = g % KCH;
-      off[u] = r * RB + ((p ^ RowTile<D>::swz(r)) * 16);
-    }
+    for (int u = 0; u < IPW; ++u) off[u] = tile_dma_offset<D, R, NW>(lane, w, u);
   }
   // resource for rows [row0, row0 + R) of a tensor with `rows` rows at `base`
   // (rows past the end read as zero; row0 >= rows copies zeros)
   __device__ __forceinline__ static i32x4 rsrc(const char* base, int row0, int rows) {
-    row0 = row0 < rows ? row0 : rows;
-    return make_rsrc(base + (size_t)row0 * RB, (uint32_t)(rows - row0) * RB);
+    const RowSpan sp = row_span(row0, rows, RB);
+    return make_rsrc(base + (size_t)sp.row0 * RB, sp.bytes);
   }
   // the u-th of this wave's IPW copy instructions (u a compile-time constant
   // after unrolling; u = 0 is the descriptor's first use)

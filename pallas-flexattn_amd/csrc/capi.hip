@@ -12,6 +12,7 @@
 
 #include "../../include/flexattn.h"
 #include "launch.h"
+#include "problem.h"
 #include "mask_build.h"
 
 // Kernels compiled at run time for one set of user mods (user_mods.h),
@@ -32,6 +33,12 @@ using fa::interval_masks;
 using fa::launch_status;
 using fa::Problem;
 using fa::Tiles;
+using fa::build_problem;
+using fa::choose_pack;
+using fa::choose_splits;
+using fa::default_tiles;
+using fa::dkdv_query_tile;
+using fa::split_bytes;
 
 // ------------------------------------------------ allocation-free bwd ----
 // fa_bwd_noalloc keeps its Delta rows (B * Hq * Sq floats) in this array
@@ -62,124 +69,6 @@ float* device_scratch() {
   return scratch_ptr[dev];
 }
 
-// The tiles of a call: the requested ones (0 = default) where an
-// instantiation exists.  bf16 interval kernels: (bm, bn) in {(128, 64),
-// (64, 64)} and, for D >= 64, {(128, 32), (128, 128), (256, 64)}; dK/dV key
-// tile bkv 128, or 64 for D >= 64.  The generic kernels (document labels
-// compared per element; every fp32 call) keep their own tiles: bm at most
-// 128, bn and bkv at the defaults.
-int default_tiles(const fa_params* p, Tiles* t) {
-  t->bm = p->block_m ? p->block_m : 128;
-  t->bkv = p->block_kv ? p->block_kv : 128;
-  if (p->dtype == FA_DTYPE_BF16) {
-    t->bn = p->block_n ? p->block_n : 64;
-    t->bq = 64;
-    if (p->q_doc_ids && !p->doc_start) {  // generic kernel
-      if (t->bm == 256) t->bm = 128;
-      t->bn = 64;
-      t->bkv = 128;
-    }
-    const bool base = (t->bm == 128 || t->bm == 64) && t->bn == 64;
-    const bool wide = (t->bm == 128 && (t->bn == 32 || t->bn == 128)) || (t->bm == 256 && t->bn == 64);
-    if (!(base || (wide && p->D >= 64))) return FA_ERR_UNSUPPORTED;
-    if (!(t->bkv == 128 || (t->bkv == 64 && p->D >= 64))) return FA_ERR_UNSUPPORTED;
-  } else if (p->dtype == FA_DTYPE_FP8_E4M3) {  // forward only: 128 x 64
-    t->bn = p->block_n ? p->block_n : 64;
-    t->bq = 64;
-    if (!(t->bm == 128 && t->bn == 64 && t->bkv == 128)) return FA_ERR_UNSUPPORTED;
-  } else {
-    t->bn = p->block_n ? p->block_n : 32;
-    t->bq = 32;
-    if (!((t->bm == 128 || t->bm == 64) && t->bn == 32 && t->bkv == 128)) return FA_ERR_UNSUPPORTED;
-  }
-  return FA_OK;
-}
-
-// Byte budgets of a head group: the L2 of one XCD is 4 MiB; q-tile walks
-// (forward, dQ) measured best at twice that (the misses hit the MALL and the
-// wider level-major groups balance the grid's tail), kv-tile walks (dK/dV) at
-// the L2 size.
-constexpr size_t kGroupBytesQ = 8u << 20;
-constexpr size_t kGroupBytesKV = 4u << 20;
-// largest power of two g dividing the heads of one XCD with g * bytes <= budget
-int head_group(int nheads, size_t bytes_per_head, size_t budget) {
-  const int hpx = nheads % 8 == 0 ? nheads / 8 : 1;
-  int g = 1;
-  while (hpx % (2 * g) == 0 && (size_t)(2 * g) * bytes_per_head <= budget) g *= 2;
-  return g;
-}
-
-int build_problem(const fa_params* p, const Tiles& t, Problem* pr) {
-  if (!p) return FA_ERR_NULL;
-  if (p->abi_version != FA_ABI_VERSION) return FA_ERR_VERSION;
-  if (p->dtype != FA_DTYPE_BF16 && p->dtype != FA_DTYPE_F32 && p->dtype != FA_DTYPE_FP8_E4M3) return FA_ERR_DTYPE;
-  if (p->B < 1 || p->Hq < 1 || p->Hkv < 1 || p->Sq < 1 || p->Skv < 1) return FA_ERR_SHAPE;
-  if (p->Hq % p->Hkv != 0) return FA_ERR_SHAPE;
-  if (p->D != 32 && p->D != 64 && p->D != 128) return FA_ERR_UNSUPPORTED;
-  if (!(p->softcap >= 0.f) || !(p->scale >= 0.f)) return FA_ERR_SHAPE;
-  if ((p->q_doc_ids == nullptr) != (p->kv_doc_ids == nullptr)) return FA_ERR_NULL;
-  Problem& r = *pr;
-  r.B = p->B;
-  r.Hq = p->Hq;
-  r.Hkv = p->Hkv;
-  r.Sq = p->Sq;
-  r.Skv = p->Skv;
-  r.scale = p->scale > 0.f ? p->scale : 1.0f / sqrtf((float)p->D);
-  r.scale_log2 = r.scale * fa::kLog2e;
-  r.win_left = p->window_left < 0 ? -1 : p->window_left;
-  r.win_right = p->window_right < 0 ? -1 : p->window_right;
-  r.q_doc = p->q_doc_ids;
-  r.kv_doc = p->kv_doc_ids;
-  if ((p->doc_start == nullptr) != (p->doc_end == nullptr)) return FA_ERR_NULL;
-  if (p->doc_start && (!p->q_doc_ids || p->Sq != p->Skv)) return FA_ERR_SHAPE;
-  r.doc_start = p->doc_start;
-  r.doc_end = p->doc_end;
-  r.alibi = p->alibi_slopes;
-  r.softcap = p->softcap;
-  r.has_mask = (r.win_left >= 0 || r.win_right >= 0 || r.q_doc != nullptr) ? 1 : 0;
-  r.xcd_remap = 1;
-  // heads per level-major group: as many as keep their K/V (forward, dQ) or
-  // Q/dO (dK/dV, all q heads of a kv head) within the group budget
-  {
-    const size_t es = p->dtype == FA_DTYPE_BF16 ? 2 : p->dtype == FA_DTYPE_F32 ? 4 : 1;
-    const size_t kv_head = 2 * (size_t)p->Skv * p->D * es / (size_t)(p->Hq / p->Hkv);
-    const size_t q_heads = 2 * (size_t)p->Sq * p->D * es * (size_t)(p->Hq / p->Hkv);
-    r.head_group_q = head_group(p->B * p->Hq, kv_head, kGroupBytesQ);
-    r.head_group_kv = head_group(p->B * p->Hkv, q_heads, kGroupBytesKV);
-  }
-  r.kv_num = p->kv_num_blocks;
-  r.kv_idx = p->kv_indices;
-  r.full_kv_num = p->full_kv_num_blocks;
-  r.full_kv_idx = p->full_kv_indices;
-  r.q_num = p->q_num_blocks;
-  r.q_idx = p->q_indices;
-  r.full_q_num = p->full_q_num_blocks;
-  r.full_q_idx = p->full_q_indices;
-  r.has_tables = (r.kv_num || r.full_kv_num || r.q_num || r.full_q_num) ? 1 : 0;
-  if (r.has_tables) {
-    if ((r.kv_num == nullptr) != (r.kv_idx == nullptr)) return FA_ERR_TABLES;
-    if ((r.full_kv_num == nullptr) != (r.full_kv_idx == nullptr)) return FA_ERR_TABLES;
-    if ((r.q_num == nullptr) != (r.q_idx == nullptr)) return FA_ERR_TABLES;
-    if ((r.full_q_num == nullptr) != (r.full_q_idx == nullptr)) return FA_ERR_TABLES;
-    if (p->mask_block_q < 1 || p->mask_block_kv < 1) return FA_ERR_TABLES;
-    if (p->table_b != 1 && p->table_b != p->B) return FA_ERR_TABLES;
-    if (p->table_h != 1 && p->table_h != p->Hq) return FA_ERR_TABLES;
-    if (p->kv_width < 0 || p->q_width < 0) return FA_ERR_TABLES;
-    r.mblk_q = p->mask_block_q;
-    r.mblk_kv = p->mask_block_kv;
-  } else {
-    r.mblk_q = t.bm;
-    r.mblk_kv = t.bn;
-  }
-  r.tab_b = p->table_b < 1 ? 1 : p->table_b;
-  r.tab_h = p->table_h < 1 ? 1 : p->table_h;
-  r.kv_width = p->kv_width;
-  r.q_width = p->q_width;
-  r.n_qblk = cdiv(p->Sq, r.mblk_q);
-  r.n_kvblk = cdiv(p->Skv, r.mblk_kv);
-  return FA_OK;
-}
-
 // Tensor rows are read and written 16 bytes per lane.
 bool aligned16(std::initializer_list<const void*> ptrs) {
   for (const void* x : ptrs)
@@ -201,12 +90,6 @@ bool has_mods(const Problem& p) { return p.alibi != nullptr || p.softcap > 0.f; 
 
 enum { kStageDelta = 1, kStageDkdv = 2, kStageDq = 4, kStageAll = 7 };
 
-// dK/dV query tile of the bf16 interval kernels: 128 rows (measured at causal
-// B4 H32 S8192 D128: step 9.10-9.14 against 9.33-9.36 ms with 64-row tiles)
-#ifndef FA_DKDV_BQ
-#define FA_DKDV_BQ 128
-#endif
-constexpr bool kDkdvQ128 = FA_DKDV_BQ == 128;
 
 template <typename T, int D, bool M>
 int bwd_all(const BwdArgs& a, const Tiles& t, int stages, hipStream_t s) {
@@ -245,17 +128,14 @@ int bwd_stages(const fa_params* p, BwdArgs& a, int stages, hipStream_t s) {
   if (rc) return rc;
   rc = build_problem(p, t, &a.p);
   if (rc) return rc;
+  rc = dkdv_query_tile(p, a.p, &t);
+  if (rc) return rc;
   if (a.p.has_tables && (stages & (kStageDkdv | kStageDq))) {
     if (a.p.mblk_q % t.bm || a.p.mblk_kv % t.bn || a.p.mblk_kv % t.bkv || a.p.mblk_q % t.bq)
       return FA_ERR_TABLES;
     if ((stages & kStageDq) && !a.p.kv_num && !a.p.full_kv_num) return FA_ERR_TABLES;
     if ((stages & kStageDkdv) && !a.p.q_num && !a.p.full_q_num) return FA_ERR_TABLES;
   }
-  // dK/dV of bf16 interval masks in 128-query tiles, where the q-side tables
-  // allow them (half the per-tile boundaries of 64-query tiles)
-  if (kDkdvQ128 && p->dtype == FA_DTYPE_BF16 && p->D >= 64 && t.bkv == 128 && interval_masks(a.p) &&
-      (!a.p.has_tables || a.p.mblk_q % 128 == 0))
-    t.bq = 128;
   const bool m = has_mods(a.p);
   if (p->dtype == FA_DTYPE_BF16)
     return m ? bwd_d<uint16_t, true>(a, p->D, t, stages, s) : bwd_d<uint16_t, false>(a, p->D, t, stages, s);
@@ -303,38 +183,6 @@ int device_cus() {
   return cached[dev];
 }
 
-// GQA row packing: for query blocks shorter than a tile, the g = Hq / Hkv
-// heads sharing a kv head run as one work item, so each K / V tile is read
-// once for the group instead of once per head (decode shapes).  Needs the
-// bf16 interval kernel and block tables (if any) shared by all heads with Sq
-// inside one mask block.
-int choose_pack(const fa_params* p, const Tiles& t, const Problem& pr) {
-  const int g = p->Hq / p->Hkv;
-  if (p->dtype != FA_DTYPE_BF16 || !interval_masks(pr) || g < 2 || p->Sq >= t.bm || t.bm != 128 || t.bn != 64)
-    return 0;
-  if (pr.has_tables && (pr.tab_h != 1 || p->Sq > pr.mblk_q)) return 0;
-  return g;
-}
-
-// Split-KV: the requested count (<= 0: about two workgroups per CU, at least
-// four key tiles per split), or 1 where the generic kernel runs.
-int choose_splits(const fa_params* p, const Tiles& t, const Problem& pr, int requested) {
-  if (p->dtype != FA_DTYPE_BF16 || !interval_masks(pr)) return 1;
-  const int items = fwd_items(pr, choose_pack(p, t, pr), t.bm);
-  const int max_by_keys = cdiv(p->Skv, 4 * t.bn);
-  int n = requested;
-  if (n <= 0) n = cdiv(2 * device_cus(), items);
-  if (n > max_by_keys) n = max_by_keys;
-  if (n > 64) n = 64;
-  return n < 1 ? 1 : n;
-}
-
-size_t split_bytes(const fa_params* p, int n) {
-  return n > 1 ? (size_t)n * p->B * p->Hq * p->Sq * (p->D + 2) * sizeof(float) : 0;
-}
-
-// The forward entry points: fa_fwd (split = false), fa_fwd_splitkv and
-// fa_fwd_kvcache (split-KV, optional paged / per-batch-length keys).
 int fwd_launch(const fa_params* p, const fa_kv_cache* kv, const void* q, const void* k, const void* v, void* o,
                float* lse, bool split, int n_splits, void* workspace, size_t workspace_bytes, void* stream) {
   if (!p) return FA_ERR_NULL;
@@ -364,7 +212,7 @@ int fwd_launch(const fa_params* p, const fa_kv_cache* kv, const void* q, const v
     a.kv_lens = kv->kv_lens;
   }
   a.pack = choose_pack(p, t, a.p);
-  a.n_splits = split ? choose_splits(p, t, a.p, n_splits) : 1;
+  a.n_splits = split ? choose_splits(p, t, a.p, n_splits, device_cus()) : 1;
   if (a.n_splits > 1) {
     if (!workspace || workspace_bytes < split_bytes(p, a.n_splits) || !aligned16({workspace}))
       return FA_ERR_WORKSPACE;
@@ -415,7 +263,7 @@ size_t fa_fwd_splitkv_workspace_bytes(const fa_params* p, int n_splits) {
   Problem pr;
   if (!p || default_tiles(p, &t) || build_problem(p, t, &pr)) return 0;
   if (n_splits > 64) return 0;
-  return split_bytes(p, choose_splits(p, t, pr, n_splits));
+  return split_bytes(p, choose_splits(p, t, pr, n_splits, device_cus()));
 }
 
 int fa_fwd_splitkv(const fa_params* p, const void* q, const void* k, const void* v, void* o, float* lse,

@@ -35,6 +35,7 @@ typedef __SIZE_TYPE__ size_t;
 #ifndef INFINITY
 #define INFINITY __builtin_inff()
 #endif
+#include "index.h"
 
 namespace fa {
 
@@ -46,6 +47,10 @@ struct Bool {
 };
 using False = Bool<false>;
 using True = Bool<true>;
+template <int N>
+struct Int {
+  static constexpr int value = N;
+};
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -57,15 +62,6 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
-
-__device__ __forceinline__ int perm23(int r) {
-  return (r & ~0xc) | ((r & 4) << 1) | ((r & 8) >> 1);
-}
-
-// physical row (within a 32-row tile) of accumulator element e held by lane half h
-__device__ __forceinline__ int acc_row(int e, int h) {
-  return 16 * (e >> 3) + 8 * h + 4 * ((e >> 2) & 1) + (e & 3);
-}
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   bf16x2_t v = {(__bf16)a, (__bf16)b};
@@ -86,37 +82,6 @@ __device__ __forceinline__ float pair_max(float x) {
 __device__ __forceinline__ float pair_sum(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-// ---- LDS tile swizzle ------------------------------------------------------
-// Row-major bf16 tiles with KCH 16-byte chunks per row store logical chunk c
-// of row r in slot c ^ chunk_swz<KCH>(r).  gfx950's LDS serves 64 banks x 4 B
-// per clock: a ds_read_b128 is conflict-free when each group of 16 lanes
-// covers 16 distinct 16-byte bank slots, a ds_read_b64_tr_b16 when each group
-// of 32 lanes (4 rows x 4 chunks) does.  With KCH = 16 (one row per 256-byte
-// bank row) the swizzle maps
-//   * the 16 rows an A-operand read takes (any 16-aligned row block, same
-//     logical chunk) to 16 distinct slots: f is a bijection on r & 15;
-//   * the 4 consecutive rows of a transposing read to 4 distinct quarter-rows:
-//     bits 2-3 of f are r & 3.
-// KCH = 8 and 4 (two / four rows per bank row) follow the same rules with the
-// row's position in the bank row taking the place of the high bits.
-template <int KCH>
-__device__ __forceinline__ int chunk_swz(int r) {
-  static_assert(KCH == 4 || KCH == 8 || KCH == 16, "chunks per row");
-  if constexpr (KCH == 16) return ((r & 3) << 2) | ((r >> 2) & 3);
-  else if constexpr (KCH == 8) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
-  else return (r >> 2) & 3;
-}
-
-// Swizzle for tiles read only by transposing reads (the forward's V): the 4
-// rows of a read land in distinct quarter-rows and rows r, r + 4 share their
-// swizzle, so a lane's addresses for rows +0..3 and +4..7 differ by a constant.
-template <int KCH>
-__device__ __forceinline__ int tr_swz(int r) {
-  if constexpr (KCH == 16) return 4 * (r & 3);
-  else if constexpr (KCH == 8) return 4 * ((r >> 1) & 1);
-  else return 0;
 }
 
 // Waves per SIMD a kernel can reach when its workgroup of NW waves holds

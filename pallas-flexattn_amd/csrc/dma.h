@@ -36,6 +36,15 @@ __device__ __forceinline__ int vload_i32(const int* base, int i, int n) {
   return raw_buffer_load_b32(make_rsrc(base, (uint32_t)n * 4u), i * 4, 0, 0);
 }
 
+// Table reads of the walks (index.h) on the device: counts through the
+// scalar cache, entries through the vector memory path (vload_i32), tile
+// starts made wave-uniform.
+struct DeviceLoad {
+  __device__ static __forceinline__ int scalar(const int* p, int i) { return scalar_load(p, i); }
+  __device__ static __forceinline__ int vector(const int* p, int i, int n) { return vload_i32(p, i, n); }
+  __device__ static __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+};
+
 __device__ __forceinline__ u32x4 buf_load16(i32x4 rsrc, int byte_off) {
   return __builtin_bit_cast(u32x4, raw_buffer_load_b128(rsrc, byte_off, 0, 0));
 }
@@ -88,6 +97,17 @@ __device__ __forceinline__ void dma16(i32x4 rsrc, int byte_off, char* lds_wave_b
 __device__ __forceinline__ void wait_vmem() {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0x0F70);
+  asm volatile("" ::: "memory");
+}
+
+// s_waitcnt vmcnt(N): every vector-memory load but the N most recent has
+// completed (loads complete in order).  With N the count of copies issued
+// for a later tile, the earlier tile's copies are done.
+template <int N>
+__device__ __forceinline__ void wait_vmem_but() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
   asm volatile("" ::: "memory");
 }
 

@@ -45,56 +45,7 @@ struct FwdArgs {
   const int* kv_lens = nullptr;
 };
 
-// A tile of a walk whose table entry may still be in flight: fetch() issues
-// the scalar load, the walk's resolve step turns the entry into a tile start
-// (an iteration or two later, so the load latency is hidden).
-struct TileRef {
-  int raw;  // table entry, still in a VGPR (dense walks: the tile number)
-  int s;    // sub-tile of the mask block
-  int hq;   // q head (q-side walks)
-};
-
-__device__ __forceinline__ int div_pow2_or(int x, int d, int d_log2) { return d_log2 >= 0 ? x >> d_log2 : x / d; }
-__device__ __forceinline__ int log2_if_pow2(int d) { return (d > 0 && (d & (d - 1)) == 0) ? __builtin_ctz(d) : -1; }
-
-// kv-tile iteration over block tables (or densely over all tiles)
-struct KvWalk {
-  const int* full;
-  const int* part;
-  int nfull, npart, sub, bn, mblk, nblk, ntiles_dense;
-  bool dense, dense_masked;
-  __device__ __forceinline__ int count() const { return dense ? ntiles_dense : (nfull + npart) * sub; }
-  // the full tiles come first in the iteration order
-  __device__ __forceinline__ int count_full() const {
-    return dense ? (dense_masked ? 0 : ntiles_dense) : nfull * sub;
-  }
-  __device__ __forceinline__ TileRef fetch(int it) const {
-    TileRef r{it, 0, 0};
-    if (!dense) {
-      const int bi = div_pow2_or(it, sub, log2_if_pow2(sub));
-      r.s = it - bi * sub;
-      r.raw = bi < nfull ? vload_i32(full, bi, nfull) : vload_i32(part, bi - nfull, npart);
-    }
-    return r;
-  }
-  __device__ __forceinline__ int kbase(const TileRef& r) const {
-    if (dense) return r.raw * bn;
-    const int raw = __builtin_amdgcn_readfirstlane(r.raw);
-    return (raw < 0 || raw >= nblk) ? kPastEnd : raw * mblk + r.s * bn;
-  }
-  __device__ __forceinline__ void get(int it, int* kbase, bool* masked) const {
-    if (dense) {
-      *kbase = it * bn;
-      *masked = dense_masked;
-      return;
-    }
-    const int bi = it / sub, s = it - bi * sub;
-    const int idx = bi < nfull ? scalar_load(full, bi) : scalar_load(part, bi - nfull);
-    *masked = bi >= nfull;
-    // an out-of-range table entry becomes a tile past the end (skipped)
-    *kbase = (idx < 0 || idx >= nblk) ? kPastEnd : idx * mblk + s * bn;
-  }
-};
+using KvWalk = KvWalkT<DeviceLoad>;
 
 // A kv walk's block indices held in one register: lane i holds entry e0 + i
 // of the row (full list first), reloaded every 64 entries, so the tiles make
@@ -114,8 +65,7 @@ struct KvTab {
     if (w.dense) return it * w.bn;
     const int bi = div_pow2_or(it, w.sub, sub_log2);
     if (bi - e0 >= 64 || bi < e0) load(w, bi & ~63, lane);
-    const int raw = __builtin_amdgcn_readlane(reg, bi - e0);
-    return (raw < 0 || raw >= w.nblk) ? kPastEnd : raw * w.mblk + (it - bi * w.sub) * w.bn;
+    return tile_start(__builtin_amdgcn_readlane(reg, bi - e0), w.nblk, w.mblk, it - bi * w.sub, w.bn);
   }
 };
 

@@ -42,9 +42,15 @@ namespace fa {
 // the training-shape forward 7 % even when unused (measured A/B).
 // Waves per SIMD: three for 32-key tiles (32 KiB of LDS; 168 registers, 8 %
 // faster than two at S = 8192, measured), two otherwise.
-template <int D, int BN, int NW, bool kMods, class Mod = BuiltinMod, bool kCache = false>
+// NS: K / V tiles in LDS at once (the tuner's stage axis).  2: double
+// buffering, the next tile copied during the current one; 3: copies two tiles
+// ahead (32-key tiles: 48 KiB, still three workgroups per CU); 1: a single
+// buffer, the next K tile copied once every wave has left the S phase and the
+// next V tile after the PV phase (128-key tiles: 64 KiB, two workgroups per CU
+// instead of one).
+template <int D, int BN, int NW, bool kMods, class Mod = BuiltinMod, bool kCache = false, int NS = 2>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(
-    occupancy_for(4 * BN * D * 2, NW, BN == 32 ? 3 : 2))))
+    occupancy_for(2 * NS * BN * D * 2, NW, BN == 32 ? 3 : 2))))
 void fwd_bf16_kernel(FwdArgs a) {
   using E = Elt<uint16_t>;
   using frag = E::frag;
@@ -58,9 +64,10 @@ void fwd_bf16_kernel(FwdArgs a) {
   constexpr int IPW = TILE / 1024 / NW; // DMA instructions per wave per tile
   static_assert(KCH >= 4 && D % 32 == 0 && BN % 32 == 0, "tile shape");
   static_assert(TILE % (1024 * NW) == 0, "DMA split");
-  static_assert(4 * BN >= BM, "O rows staged through the K / V buffers");
+  static_assert(NS >= 1 && NS <= 3 && (!kCache || NS == 2), "LDS stages");
+  static_assert(2 * NS * BN >= BM, "O rows staged through the K / V buffers");
 
-  __shared__ __attribute__((aligned(1024))) char lds[4 * TILE];  // K0 K1 V0 V1
+  __shared__ __attribute__((aligned(1024))) char lds[2 * NS * TILE];  // K_0 .. K_{NS-1}, V_0 .. V_{NS-1}
 
   const Problem& P = a.p;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -111,31 +118,21 @@ void fwd_bf16_kernel(FwdArgs a) {
   key_interval(P, b, qw, &klo, &khi);
   khi = min(khi, skv - 1);
 
-  // loop-invariant LDS / global offsets
+  // loop-invariant LDS / global offsets (index.h)
   int dma_off_k[IPW], dma_off_v[IPW];
 #pragma unroll
   for (int u = 0; u < IPW; ++u) {
-    const int g = (w * IPW + u) * 64 + lane;
-    const int r = g / KCH, p = g % KCH;
-    dma_off_k[u] = r * RB + ((p ^ chunk_swz<KCH>(r)) * 16);
-    dma_off_v[u] = r * RB + ((p ^ tr_swz<KCH>(r)) * 16);
+    dma_off_k[u] = tile_dma_offset<D, BN, NW>(lane, w, u);
+    dma_off_v[u] = tile_dma_offset<D, BN, NW, true>(lane, w, u);
   }
-  int koffA[KSTEPS];
-  {
-    const int r = perm23(lr);
-#pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) koffA[s] = r * RB + (((2 * s + hh) ^ chunk_swz<KCH>(r)) * 16);
-  }
+  RowTileOffsets<D> kt;  // K read as A operand rows (aoff)
+  kt.init(lane);
+  const int* koffA = kt.aoff;
   // transposing reads of V: rows row + 16c (+4 for the upper half of the
   // fragment), chunk 4i + x of d tile i
   int voffT[DT];
-  {
-    const int s16 = lane & 15, g = lane >> 4;
-    const int row = 8 * (g >> 1) + (s16 >> 2);
-    const int x = 2 * (g & 1) + ((s16 & 3) >> 1);
 #pragma unroll
-    for (int i = 0; i < DT; ++i) voffT[i] = row * RB + (((4 * i + x) ^ tr_swz<KCH>(row)) * 16) + (s16 & 1) * 8;
-  }
+  for (int i = 0; i < DT; ++i) voffT[i] = fwd_voff_t<D>(lane, i);
 
   KvWalk walk;
   walk.bn = BN;
@@ -169,24 +166,25 @@ void fwd_bf16_kernel(FwdArgs a) {
   // hundreds of cycles (1.5 % of the forward at S = 8192, measured).
   struct Copy { i32x4 rk, rv; char* kl; char* vl; };
   auto issue_plan = [&](int kb, int buf) {
-    kb = kb < skv ? kb : skv;
+    const RowSpan sp = row_span(kb, skv, RB);
+    kb = sp.row0;
     const char* kp = kbase_ptr + (size_t)kb * RB;
     const char* vp = vbase_ptr + (size_t)kb * RB;
-    uint32_t range = (uint32_t)(skv - kb) * RB;
+    uint32_t range = sp.bytes;
     if (kCache && a.page_table) {  // the tile lies inside one page (page_size is a multiple of BN)
-      const int pg = kb / a.page_size, off = kb - pg * a.page_size;
+      // a bad page id reads zeros (index.h: page_span)
+      const int pg = kb / a.page_size;
       const int phys = kb < skv ? scalar_load(a.page_table + (size_t)b * a.max_pages, pg) : -1;
-      const bool ok = phys >= 0 && phys < a.num_pages;  // a bad page id reads zeros
-      const size_t at = ((size_t)(ok ? phys : 0) * P.Hkv + hk) * a.page_size + off;
-      kp = static_cast<const char*>(a.k) + at * RB;
-      vp = static_cast<const char*>(a.v) + at * RB;
-      range = ok ? (uint32_t)min(a.page_size - off, skv - kb) * RB : 0u;
+      const PageSpan ps = page_span(kb, pg, skv, a.page_size, phys, a.num_pages, P.Hkv, hk);
+      kp = static_cast<const char*>(a.k) + ps.row * RB;
+      vp = static_cast<const char*>(a.v) + ps.row * RB;
+      range = (uint32_t)ps.rows * RB;
     }
     Copy c;
     c.rk = make_rsrc(kp, range);
     c.rv = make_rsrc(vp, range);
     c.kl = lds + buf * TILE;
-    c.vl = lds + (2 + buf) * TILE;
+    c.vl = lds + (NS + buf) * TILE;
     return c;
   };
   auto issue_one = [&](const Copy& c, int i) {
@@ -292,29 +290,36 @@ void fwd_bf16_kernel(FwdArgs a) {
   const int sub_log2 = log2_if_pow2(walk.sub);
   KvTab tab;
   auto kbase_of = [&](int it) { return tab.kbase(walk, it, sub_log2, lane); };
-  if (it0 < it1) issue(kbase_of(it0), 0);
+  // the first NS - 1 tiles (with one buffer, the first) copied ahead
+  constexpr int AHEAD = NS > 1 ? NS - 1 : 1;
+#pragma unroll
+  for (int i = 0; i < AHEAD; ++i)
+    if (it0 + i < it1) issue(kbase_of(it0 + i), i);
   // unconditional, so the wait-count analysis sees the register loads above
   // complete on every path into the loop
   wait_vmem();
   __syncthreads();
-  // One tile; buf_c (the LDS buffer the tile sits in) is a compile-time
-  // constant, so every LDS operand address is a per-lane register plus an
-  // immediate offset (the loop below runs tiles in pairs).
+  // One tile; buf_c (the LDS buffer the tile sits in, tile it0 + i in buffer
+  // i % NS) is a compile-time constant, so every LDS operand address is a
+  // per-lane register plus an immediate offset (the loop below runs NS tiles
+  // per iteration).
   auto tile_step = [&](int it, auto buf_c) {
     constexpr int buf = decltype(buf_c)::value;
     const int kbase = kbase_of(it);
     bool masked = it >= n_full;
-    const bool more = it + 1 < it1;
+    // the tile copied during this one: AHEAD tiles ahead, into the buffer
+    // read last in the previous tile (NS = 1: the same buffer, in two halves)
+    const bool more = it + AHEAD < it1;
     Copy nc;
-    if (more) nc = issue_plan(kbase_of(it + 1), buf ^ 1);
-    if (kbase >= skv && more) {
+    if (more) nc = issue_plan(kbase_of(it + AHEAD), (buf + AHEAD) % NS);
+    if (NS > 1 && kbase >= skv && more) {
 #pragma unroll
       for (int i = 0; i < 2 * IPW; ++i) issue_one(nc, i);
     }
     if (kbase < skv) {  // workgroup-uniform
       masked = masked || (kbase + BN > skv);
       const char* kl = lds + buf * TILE;
-      const char* vl = lds + (2 + buf) * TILE;
+      const char* vl = lds + (NS + buf) * TILE;
 
       f32x16 sacc[NSUB];
 #pragma unroll
@@ -340,12 +345,22 @@ void fwd_bf16_kernel(FwdArgs a) {
 #pragma unroll
         for (int j = 0; j < NSUB; ++j) sacc[j] = E::mma(ka[s % KR][j], qf[s], sacc[j]);
         // this k step's share of the next tile's copies
+        if constexpr (NS > 1) {
 #pragma unroll
-        for (int i = 0; i < 2 * IPW; ++i)
-          if (i * KSTEPS / (2 * IPW) == s && more) issue_one(nc, i);
+          for (int i = 0; i < 2 * IPW; ++i)
+            if (i * KSTEPS / (2 * IPW) == s && more) issue_one(nc, i);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
       if (FA_FWD_PRIO) __builtin_amdgcn_s_setprio(0);
+      if constexpr (NS == 1) {
+        // every wave is past its K reads: the next K tile goes into the buffer
+        __syncthreads();
+        if (more) {
+#pragma unroll
+          for (int i = 0; i < IPW; ++i) issue_one(nc, i);
+        }
+      }
 
       if constexpr (kMods && !Mod::kScore) {
         // built-in ALiBi + soft-cap: slope (k - q) = slope (base_j + c_e) with
@@ -428,15 +443,44 @@ void fwd_bf16_kernel(FwdArgs a) {
       }
       if (FA_FWD_PRIO) __builtin_amdgcn_s_setprio(0);
     }
-    wait_vmem();
+    if constexpr (NS == 1) {
+      // every wave is past its V reads: the next V tile (and, for a tile
+      // past the keys, the K tile not copied above), then wait for both
+      __syncthreads();
+      if (more) {
+#pragma unroll
+        for (int i = 0; i < 2 * IPW; ++i)
+          if (i >= IPW || kbase >= skv) issue_one(nc, i);
+      }
+      wait_vmem();
+    } else if constexpr (NS == 2) {
+      wait_vmem();
+    } else {
+      // the next tile's copies (issued a tile earlier) are done once at most
+      // this tile's 2 * IPW copies remain
+      if (more) wait_vmem_but<2 * IPW>();
+      else wait_vmem();
+    }
     __syncthreads();
   };
   int it = it0;
-  for (; it + 1 < it1; it += 2) {
-    tile_step(it, Bool<0>{});
-    tile_step(it + 1, Bool<1>{});
+  if constexpr (NS == 1) {
+    for (; it < it1; ++it) tile_step(it, Int<0>{});
+  } else if constexpr (NS == 2) {
+    for (; it + 1 < it1; it += 2) {
+      tile_step(it, Int<0>{});
+      tile_step(it + 1, Int<1>{});
+    }
+    if (it < it1) tile_step(it, Int<0>{});
+  } else {
+    for (; it + 2 < it1; it += 3) {
+      tile_step(it, Int<0>{});
+      tile_step(it + 1, Int<1>{});
+      tile_step(it + 2, Int<2>{});
+    }
+    if (it < it1) tile_step(it, Int<0>{});
+    if (it + 1 < it1) tile_step(it + 1, Int<1>{});
   }
-  if (it < it1) tile_step(it, Bool<0>{});
 
 #pragma unroll
   for (int i = 0; i < DT; ++i) mfma_drain<FA_FWD_OREG>(oacc[i]);

@@ -5,40 +5,6 @@
 
 namespace fa {
 
-// Everything a kernel needs to know about the attention problem except the
-// tensor pointers.  Built on the host from fa_params.
-struct Problem {
-  int B, Hq, Hkv, Sq, Skv;
-  float scale;       // softmax scale applied to q.k
-  float scale_log2;  // scale * log2(e)
-  // mask: window on delta = q - kv (left/right < 0: unlimited) and documents
-  int win_left, win_right;
-  const int* q_doc;   // (B, Sq) or null
-  const int* kv_doc;  // (B, Skv) or null
-  // contiguous documents (self-attention): token t's document is
-  // [doc_start[b][t], doc_end[b][t]); when set, masks are key/query intervals
-  const int* doc_start;
-  const int* doc_end;
-  // score modification: s += alibi[h] * (kv - q); then s = cap * tanh(s / cap)
-  const float* alibi;  // (Hq) or null
-  float softcap;       // <= 0: off
-  // block tables at mask-block granularity (PyTorch BlockMask convention:
-  // kv_* lists the partial blocks, full_kv_* the fully-live ones)
-  const int *kv_num, *kv_idx, *full_kv_num, *full_kv_idx;  // rows = q mask blocks
-  const int *q_num, *q_idx, *full_q_num, *full_q_idx;      // rows = kv mask blocks
-  int tab_b, tab_h;      // 1 or B, 1 or Hq
-  int n_qblk, n_kvblk;   // table rows (q side / kv side)
-  int kv_width, q_width;
-  int mblk_q, mblk_kv;   // mask block sizes
-  int has_tables;        // 0: dense iteration over all blocks
-  int has_mask;          // any window / doc term active
-  int xcd_remap;         // group work of a head onto one XCD
-  int head_group_q;      // heads per level-major group, q-tile walks (forward, dQ)
-  int head_group_kv;     // the same for kv-tile walks (dK/dV)
-  // tensors read by user score / mask mods compiled at run time (see Mod below)
-  const void* mod_buf[8];
-};
-
 // Element policy of the kernels.  BuiltinMod: the element mask is the window
 // / document terms of the Problem and the score epilogue its ALiBi + soft-cap.
 // A policy compiled at run time from user mods (fa_mods_build) has the same
@@ -75,31 +41,6 @@ __device__ __forceinline__ bool mask_ok(const Problem& p, int q, int k, int qdoc
 // and/or contiguous documents); false for arbitrary document labels.
 __device__ __forceinline__ bool interval_mask(const Problem& p) {
   return p.q_doc == nullptr || p.doc_start != nullptr;
-}
-
-// Keys visible to query q: [lo, hi] (empty when lo > hi).  With delta = q - k,
-// delta <= left gives k >= q - left and -delta <= right gives k <= q + right.
-__device__ __forceinline__ void key_interval(const Problem& p, int b, int q, int* lo, int* hi) {
-  int l = p.win_left >= 0 ? q - p.win_left : 0;
-  int h = p.win_right >= 0 ? q + p.win_right : p.Skv - 1;
-  if (p.doc_start != nullptr && q < p.Sq) {
-    l = max(l, p.doc_start[(size_t)b * p.Sq + q]);
-    h = min(h, p.doc_end[(size_t)b * p.Sq + q] - 1);
-  }
-  *lo = max(l, 0);
-  *hi = q < p.Sq ? min(h, p.Skv - 1) : -1;
-}
-
-// Queries that see key k: [lo, hi] (q <= k + left, q >= k - right).
-__device__ __forceinline__ void query_interval(const Problem& p, int b, int k, int* lo, int* hi) {
-  int l = p.win_right >= 0 ? k - p.win_right : 0;
-  int h = p.win_left >= 0 ? k + p.win_left : p.Sq - 1;
-  if (p.doc_start != nullptr && k < p.Skv) {
-    l = max(l, p.doc_start[(size_t)b * p.Skv + k]);
-    h = min(h, p.doc_end[(size_t)b * p.Skv + k] - 1);
-  }
-  *lo = max(l, 0);
-  *hi = k < p.Skv ? min(h, p.Sq - 1) : -1;
 }
 
 __device__ __forceinline__ int kv_doc_of(const Problem& p, int b, int k) {
@@ -182,43 +123,6 @@ template <class Mod>
 __device__ __forceinline__ bool mod_mask_ok(const Problem& P, int b, int h, int q, int k, int qdoc, int kdoc) {
   if constexpr (Mod::kMask) return mask_ok(P, q, k, qdoc, kdoc) && Mod::mask(P, b, h, q, k);
   else return mask_ok(P, q, k, qdoc, kdoc);
-}
-
-// Tile start used for out-of-range table entries: beyond any sequence, so the
-// tile is skipped and its loads are predicated off.
-constexpr int kPastEnd = 0x40000000;
-
-__device__ __forceinline__ int clamp_count(int n, int width) { return n < 0 ? 0 : (n > width ? width : n); }
-
-// Row of the block tables for (b, h, row).
-__device__ __forceinline__ int tab_row(const Problem& p, int b, int h, int row, int nrows) {
-  const int tb = p.tab_b == 1 ? 0 : b;
-  const int th = p.tab_h == 1 ? 0 : h;
-  return (tb * p.tab_h + th) * nrows + row;
-}
-
-// Work-item order: blockIdx.x is dispatched round-robin over the 8 XCDs.  With
-// remapping, XCD x processes heads [x*H/8, (x+1)*H/8) in groups of `group`
-// heads, one group after another, so the K/V (or Q/dO) of a group stay in
-// that XCD's L2 while its tiles run (the host sizes groups to the L2).  Inside
-// a group the tiles go level by level across its heads, the longest walks
-// first (causal: the last q tiles, or with low_first the first kv tiles), so
-// the short tiles fill the end of the grid.
-__device__ __forceinline__ void work_item(int bid, int nheads, int ntiles, bool remap, int group, bool low_first,
-                                          int* head, int* tile) {
-  int t;
-  if (remap && (nheads % 8) == 0) {
-    const int xcd = bid & 7, slot = bid >> 3;
-    const int hpx = nheads >> 3;
-    const int per_group = group * ntiles;
-    const int gi = slot / per_group, r = slot - gi * per_group;
-    *head = xcd * hpx + gi * group + r % group;
-    t = r / group;
-  } else {
-    *head = bid / ntiles;
-    t = bid % ntiles;
-  }
-  *tile = low_first ? t : ntiles - 1 - t;
 }
 
 }  // namespace fa

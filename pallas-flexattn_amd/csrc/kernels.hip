@@ -17,7 +17,7 @@ constexpr bool generic_tile() {
   return BN == (sizeof(T) == 2 ? 64 : 32) && NW <= 4;
 }
 
-template <typename T, int D, int BN, int NW, bool M>
+template <typename T, int D, int BN, int NW, bool M, int NS = 2>
 int run_fwd(const FwdArgs& a, hipStream_t s) {
   const int grid = fwd_items(a.p, a.pack, 32 * NW);
   if constexpr (sizeof(T) == 2) {
@@ -39,7 +39,8 @@ int run_fwd(const FwdArgs& a, hipStream_t s) {
           hipLaunchKernelGGL((fa::fwd_bf16_kernel<D, BN, NW, M>), dim3(grid * a.n_splits), dim3(NW * 64), 0, s, a);
       } else {
         if (cache) return FA_ERR_UNSUPPORTED;  // the KV-cache variant has 128 x 64 tiles
-        hipLaunchKernelGGL((fa::fwd_bf16_kernel<D, BN, NW, M>), dim3(grid * a.n_splits), dim3(NW * 64), 0, s, a);
+        hipLaunchKernelGGL((fa::fwd_bf16_kernel<D, BN, NW, M, fa::BuiltinMod, false, NS>), dim3(grid * a.n_splits),
+                           dim3(NW * 64), 0, s, a);
       }
       if (a.n_splits > 1) {
         const size_t n = (size_t)a.p.B * a.p.Hq * a.p.Sq * D;
@@ -48,7 +49,7 @@ int run_fwd(const FwdArgs& a, hipStream_t s) {
       return launch_status();
     }
   }
-  if constexpr (generic_tile<T, BN, NW>()) {
+  if constexpr (generic_tile<T, BN, NW>() && NS == 2) {
     FwdArgs g = a;  // the generic kernel has no split-KV, packed or paged form
     g.n_splits = 1;
     g.pack = 0;
@@ -62,8 +63,9 @@ template <typename T, int D, bool M>
 int launch_fwd(const FwdArgs& a, const Tiles& t, hipStream_t s) {
   if constexpr (sizeof(T) == 2) {
     if constexpr (D >= 64) {
-      if (t.bn == 32) return run_fwd<T, D, 32, 4, M>(a, s);
-      if (t.bn == 128) return run_fwd<T, D, 128, 4, M>(a, s);
+      // LDS stages: 3 with 32-key tiles, 1 with 128-key tiles, else 2
+      if (t.bn == 32) return t.ns == 3 ? run_fwd<T, D, 32, 4, M, 3>(a, s) : run_fwd<T, D, 32, 4, M>(a, s);
+      if (t.bn == 128) return t.ns == 1 ? run_fwd<T, D, 128, 4, M, 1>(a, s) : run_fwd<T, D, 128, 4, M>(a, s);
       if (t.bm == 256) return run_fwd<T, D, 64, 8, M>(a, s);
     }
     return t.bm == 64 ? run_fwd<T, D, 64, 2, M>(a, s) : run_fwd<T, D, 64, 4, M>(a, s);
@@ -74,7 +76,7 @@ int launch_fwd(const FwdArgs& a, const Tiles& t, hipStream_t s) {
 
 template <typename T, int D, int BN, int NW, bool M>
 int run_dq(const BwdArgs& a, hipStream_t s) {
-  const int grid = a.p.B * a.p.Hq * cdiv(a.p.Sq, 32 * NW);
+  const int grid = dq_grid(a.p, 32 * NW);
   if constexpr (sizeof(T) == 2) {
     if (interval_masks(a.p)) {
       hipLaunchKernelGGL((fa::dq_bf16_kernel<D, BN, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);
@@ -90,7 +92,7 @@ int run_dq(const BwdArgs& a, hipStream_t s) {
 
 template <typename T, int D, int BQ, int NW, bool M>
 int run_dkdv(const BwdArgs& a, hipStream_t s) {
-  const int grid = a.p.B * a.p.Hkv * cdiv(a.p.Skv, 32 * NW);
+  const int grid = dkdv_grid(a.p, 32 * NW);
   if constexpr (sizeof(T) == 2) {
     if (interval_masks(a.p)) {
       hipLaunchKernelGGL((fa::dkdv_bf16_kernel<D, BQ, NW, M>), dim3(grid), dim3(NW * 64), 0, s, a);

@@ -9,27 +9,11 @@
 #include "bwd.h"
 #include "fwd.h"
 #include "fwd_fp8.h"
+#include "problem.h"
 
 namespace fa {
 
-struct Tiles {
-  int bm, bn;    // forward / dQ: query tile, key tile
-  int bkv, bq;   // dK/dV: key tile, query tile
-};
-
-inline int cdiv(int a, int b) { return (a + b - 1) / b; }
-
 inline int launch_status() { return hipGetLastError() == hipSuccess ? FA_OK : FA_ERR_LAUNCH; }
-
-// The bf16 LDS-DMA kernels evaluate masks as per-lane intervals (windows and
-// contiguous documents); arbitrary document labels go to the generic kernels.
-inline bool interval_masks(const Problem& p) { return p.q_doc == nullptr || p.doc_start != nullptr; }
-
-// Work items of the forward: (batch, q head, query tile), or with GQA row
-// packing (batch, kv head, tile of the group's g * Sq rows).
-inline int fwd_items(const Problem& p, int pack, int bm) {
-  return pack > 1 ? p.B * p.Hkv * cdiv(pack * p.Sq, bm) : p.B * p.Hq * cdiv(p.Sq, bm);
-}
 
 // Element type T (uint16_t: bf16, float), head dim D, with (M) or without
 // the built-in score mods (ALiBi, soft-cap); tiles as chosen by the C ABI.

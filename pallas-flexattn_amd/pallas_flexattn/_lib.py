@@ -10,7 +10,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 # FLEXATTN_LIB names another build of the same library (same ABI), e.g. to
 # time two builds side by side in one process tree.
 LIB_PATH = os.environ.get("FLEXATTN_LIB") or os.path.join(_HERE, "libflexattn.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_BF16 = 0
 DTYPE_F32 = 1
@@ -40,6 +40,7 @@ class FaParams(ctypes.Structure):
         ("full_kv_num_blocks", _pi32), ("full_kv_indices", _pi32),
         ("q_num_blocks", _pi32), ("q_indices", _pi32),
         ("full_q_num_blocks", _pi32), ("full_q_indices", _pi32),
+        ("block_q", _i32), ("lds_stages", _i32),
     ]
 
 

@@ -32,7 +32,7 @@ import numpy as np
 from . import _lib, lowering
 from .block_mask import BlockMask, _finish, create_block_mask
 from .kernel_tuner import (DEFAULT_BLOCK_C, DEFAULT_BLOCK_R, DEFAULT_NUM_STAGES, DEFAULT_NUM_WARPS, DEFAULT_TILES,
-                           kernel_tiles, tuned_tiles)
+                           TILE_NAMES, full_tiles, kernel_tiles, mask_class, tuned_tiles)
 from .mask_mod import MaskSpec, MaskMod, and_masks, causal_mask, document_ids_mask
 from .score_mod import ScoreSpec
 
@@ -95,7 +95,7 @@ class _Plan:
     so repeated calls make no host-to-device copies."""
 
     def __init__(self, q, k, mask: Optional[MaskSpec], score: Optional[ScoreSpec], scale: Optional[float],
-                 block_mask: Optional[BlockMask], tiles: Tuple[int, int, int]):
+                 block_mask: Optional[BlockMask], tiles: Tuple[int, ...]):
         B, Hq, Sq, D = q.shape
         Hkv, Skv = k.shape[1], k.shape[2]
         code, dname = _dtype_code(q)
@@ -103,7 +103,9 @@ class _Plan:
         p.abi_version = _lib.ABI_VERSION
         p.dtype = code
         p.B, p.Hq, p.Hkv, p.Sq, p.Skv, p.D = B, Hq, Hkv, Sq, Skv, D
-        p.block_m, p.block_n, p.block_kv = tiles
+        p.block_m, p.block_n, p.block_kv = tiles[:3]
+        p.block_q = tiles[3] if len(tiles) > 3 else 0
+        p.lds_stages = tiles[4] if len(tiles) > 4 else 0
         p.scale = 0.0 if scale is None else float(scale)
         p.window_left = p.window_right = -1
         self.keep = []
@@ -460,15 +462,19 @@ def _bwd_core(q, k, v, o, lse, do, mask, score, scale, block_mask, tiles, mods=N
 _MODS_TILES = {"bf16": (128, 64, 128), "fp32": (128, 32, 128)}
 
 
-def _sparse(mask) -> bool:
-    return mask is not None and not mask.is_trivial
+class _AnyMask:
+    """Stands for a traced user mask when picking tiles (causal class)."""
+    left, right, doc_ids = -1, 0, None
 
 
-def _ref_tiles(q, block_r, block_c, sparse=False):
-    """Kernel tile of a reference-signature call: block_r / block_c are
-    Triton hints; the tuned tile for the shape class (or the default) runs."""
+_ANY_MASK = _AnyMask()
+
+
+def _ref_tiles(q, block_r, block_c, mask=None):
+    """Kernel tiles of a reference-signature call: block_r / block_c are
+    Triton hints; the tuned tiles for the shape class (or the defaults) run."""
     _, dname = _dtype_code(q)
-    return kernel_tiles(block_r, block_c, dname, q.shape[2], q.shape[3], sparse)
+    return kernel_tiles(block_r, block_c, dname, q.shape[2], q.shape[3], mask_class(mask))
 
 
 def _as4d(t):
@@ -480,7 +486,7 @@ def _stage_plan(q4, k4, mask_mod, block_r, block_c, scale=None):
     """(plan, user mods) of a reference-signature backward stage."""
     mask, _, mods = _resolve(mask_mod, None)
     tiles = _MODS_TILES[_dtype_code(q4)[1]] if mods is not None else \
-        _ref_tiles(q4, block_r, block_c, _sparse(mask) or (mods is not None and mods.mask is not None))
+        _ref_tiles(q4, block_r, block_c, mask if mods is None or mods.mask is None else _ANY_MASK)
     bm, tiles = _tables_for(mask, mods, None, q4, k4, tiles)
     return _get_plan(q4, k4, mask, None, scale, bm, tiles), mods
 
@@ -579,9 +585,9 @@ class Runner:
             raise NotImplementedError("Runner takes the built-in mask / score descriptors; use flex_attention for "
                                       "user callables")
         _, dname = _dtype_code(q)
-        tiles = tuple(tiles or DEFAULT_TILES[dname])
-        if len(tiles) == 2:
-            tiles = tiles + (DEFAULT_TILES[dname][2],)
+        if tiles is None:  # the tuned tiles of the shape class, as flex_attention picks them
+            tiles = tuned_tiles(q.shape[2], q.shape[3], dname, mask_class(mask)) or DEFAULT_TILES[dname]
+        tiles = full_tiles(tiles, dname)
         block_mask, tiles = _tables_for(mask, None, block_mask, self.q, self.k, tiles)
         self.plan = _Plan(self.q, self.k, mask, score, scale, block_mask, tiles)
         self.block_mask = block_mask
@@ -654,7 +660,7 @@ def flash_attention_fwd(q, k, v, mask_mod: Optional[MaskMod] = None, block_r: in
     """Forward pass -> (o, logsumexp) with logsumexp in q's dtype (``flash_attn.py:111-165``)."""
     host = _check_interpret(interpret, q)
     mask, _, mods = _resolve(mask_mod, None)
-    o, lse, _ = _fwd_core(q, k, v, mask, None, None, None, _ref_tiles(q, block_r, block_c, _sparse(mask)), mods,
+    o, lse, _ = _fwd_core(q, k, v, mask, None, None, None, _ref_tiles(q, block_r, block_c, mask), mods,
                           host)
     return o, lse.to(q.dtype)
 
@@ -668,7 +674,7 @@ def flash_attention_bwd(q, k, v, o, logsumexp, do, mask_mod: Optional[MaskMod] =
     host = _check_interpret(interpret, q)
     mask, _, mods = _resolve(mask_mod, None)
     return _bwd_core(q, k, v, o, logsumexp, do, mask, None, None, None,
-                     _ref_tiles(q, block_r, block_c, _sparse(mask)), mods, host)
+                     _ref_tiles(q, block_r, block_c, mask), mods, host)
 
 
 class _FlexFn:
@@ -708,7 +714,7 @@ def flash_attention(q, k, v, mask_mod: Optional[MaskMod] = None, block_r: int = 
     """Flash attention with a custom backward (``flash_attn.py:464-504``)."""
     host = _check_interpret(interpret, q)
     mask, _, mods = _resolve(mask_mod, None)
-    cfg = (mask, None, None, None, _ref_tiles(q, block_r, block_c, _sparse(mask)), mods, host)
+    cfg = (mask, None, None, None, _ref_tiles(q, block_r, block_c, mask), mods, host)
     o, _ = _FlexFn.get().apply(q, k, v, cfg)
     return o
 
@@ -867,9 +873,12 @@ def flex_attention(query, key, value, score_mod: Optional[ScoreSpec] = None,
     blocks of ``block_mask`` (all blocks when None).  Differentiable.
 
     ``kernel_options`` may set ``BLOCK_M`` (query rows per forward / dQ
-    workgroup, 32 per wave), ``BLOCK_N`` (keys per LDS tile) and ``BLOCK_KV``
-    (keys per dK/dV workgroup); otherwise the tuned table entry for the shape
-    class or the defaults (bf16: 128 x 64 / 128, fp32: 128 x 32 / 128) run."""
+    workgroup, 32 per wave), ``BLOCK_N`` (keys per LDS tile), ``BLOCK_KV``
+    (keys per dK/dV workgroup), ``BLOCK_Q`` (queries per dK/dV tile, 64 or
+    128) and ``NUM_STAGES`` (K / V tiles the forward holds in LDS: 2, 3 with
+    ``BLOCK_N`` 32, 1 with ``BLOCK_N`` 128); otherwise the tuned table entry
+    for the shape class (dtype, head dim, length, mask class) or the defaults
+    (bf16: 128 x 64 / 128 with automatic q tiles, fp32: 128 x 32 / 128) run."""
     if query.shape[1] != key.shape[1] and not enable_gqa:
         raise ValueError("query and key head counts differ: pass enable_gqa=True for grouped-query attention")
     mask_mod = None
@@ -881,9 +890,10 @@ def flex_attention(query, key, value, score_mod: Optional[ScoreSpec] = None,
     # tables at another block size are re-derived for the kernel tiles (_tables_for)
     _, dname = _dtype_code(query)
     opts = kernel_options or {}
-    tiles = tuned_tiles(query.shape[2], query.shape[3], dname, block_mask is not None) or DEFAULT_TILES[dname]
-    if any(o in opts for o in ("BLOCK_M", "BLOCK_N", "BLOCK_KV")):
-        tiles = tuple(int(opts.get(o, d)) for o, d in zip(("BLOCK_M", "BLOCK_N", "BLOCK_KV"), DEFAULT_TILES[dname]))
+    cls = mask_class(mask) if mods is None or mods.mask is None else "causal"
+    tiles = tuned_tiles(query.shape[2], query.shape[3], dname, cls) or DEFAULT_TILES[dname]
+    if any(o in opts for o in TILE_NAMES):
+        tiles = tuple(int(opts.get(o, d)) for o, d in zip(TILE_NAMES, DEFAULT_TILES[dname]))
     cfg = (mask, score, scale, block_mask, tiles, mods, False)
     o, lse = _FlexFn.get().apply(query, key, value, cfg)
     return (o, lse) if return_lse else o

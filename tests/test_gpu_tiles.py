@@ -1,7 +1,8 @@
-"""Every tile configuration the tuner can pick (BLOCK_M x BLOCK_N x BLOCK_KV
-of the bf16 kernels: 2, 4 or 8 waves per forward / dQ workgroup, 32, 64 or
-128 keys per LDS tile, 2 or 4 waves per dK/dV workgroup) on the GPU, forward
-and backward through flex_attention's kernel_options, against the float64
+"""Every tile configuration the tuner can pick (BLOCK_M x BLOCK_N x BLOCK_KV x
+BLOCK_Q x NUM_STAGES of the bf16 kernels: 2, 4 or 8 waves per forward / dQ
+workgroup, 32, 64 or 128 keys per LDS tile, 1, 2 or 3 K / V tiles in LDS,
+2 or 4 waves per dK/dV workgroup, 64 or 128 queries per dK/dV tile) on the
+GPU, forward and backward through flex_attention's kernel_options, against the float64
 oracle at bf16 atol = rtol = 2e-2.  The masks rotate over the tile sets so
 each set meets a different one (causal, window, contiguous documents, none
 with ragged lengths, Sq != Skv), with GQA and ALiBi + soft-cap on some; the
@@ -68,7 +69,8 @@ def test_tiles_fwd_bwd(case):
         alibi, softcap = pf.alibi_slopes(Hq), 30.0
         score = pf.compose_score_mods(pf.alibi_score_mod(alibi), pf.softcap_score_mod(softcap))
     bm = pf.create_block_mask(mm, B, Hq, Sq, Skv, 128) if mm is not None else None
-    opts = dict(zip(("BLOCK_M", "BLOCK_N", "BLOCK_KV"), tiles))
+    from pallas_flexattn.kernel_tuner import TILE_NAMES
+    opts = dict(zip(TILE_NAMES, tiles))
     tq, tk, tv = (to_torch(x, "bf16").requires_grad_() for x in (q, k, v))
     o, lse = pf.flex_attention(tq, tk, tv, score_mod=score, block_mask=bm, enable_gqa=Hq != Hkv, return_lse=True,
                                kernel_options=opts)
@@ -80,10 +82,10 @@ def test_tiles_fwd_bwd(case):
         assert_close(f"{name} {nm}", to_np(got), want, BF16_TOL)
 
 
-FWD_TILES = [(128, 32), (128, 128), (256, 64), (64, 64)]
+FWD_TILES = [(128, 32, 2), (128, 32, 3), (128, 128, 2), (128, 128, 1), (256, 64, 2), (64, 64, 2)]
 
 
-@pytest.mark.parametrize("fwd_tiles", FWD_TILES, ids=[f"{a}x{b}" for a, b in FWD_TILES])
+@pytest.mark.parametrize("fwd_tiles", FWD_TILES, ids=[f"{a}x{b}s{c}" for a, b, c in FWD_TILES])
 def test_tiles_forward_rescale_path(fwd_tiles):
     """Logits growing along the keys (the running maximum rises by more than
     16 in log2 units between tiles) and huge logits (exponentials overflow
@@ -92,7 +94,7 @@ def test_tiles_forward_rescale_path(fwd_tiles):
     import pallas_flexattn as pf
     from oracle.bf16 import round_bf16
     B, H, S, D = 1, 2, 512, 128
-    opts = {"BLOCK_M": fwd_tiles[0], "BLOCK_N": fwd_tiles[1]}
+    opts = {"BLOCK_M": fwd_tiles[0], "BLOCK_N": fwd_tiles[1], "NUM_STAGES": fwd_tiles[2]}
     for name, kind, qscale, ramp in (("growing-causal", "causal", 2.0, 3.0), ("huge-dense", None, 64.0, 0.0)):
         print(f"[gpu tiles] rescale {name} {fwd_tiles}", flush=True)
         q, k, v, do = inputs(zlib.crc32(name.encode()) % 1000, B, H, H, S, S, D, "fp32")
@@ -120,6 +122,14 @@ def test_tiles_reach_the_c_abi():
     q = torch.randn(1, 2, 256, 32, device="cuda", dtype=torch.bfloat16)
     with pytest.raises(_lib.FlexAttnError):
         pf.flex_attention(q, q, q, kernel_options={"BLOCK_M": 128, "BLOCK_N": 128})  # D = 32: 64-key tiles only
+    x = torch.randn(1, 2, 256, 64, device="cuda", dtype=torch.bfloat16)
+    for bad in ({"NUM_STAGES": 3}, {"BLOCK_N": 128, "NUM_STAGES": 3}, {"BLOCK_N": 32, "NUM_STAGES": 1},
+                {"BLOCK_Q": 96}):
+        with pytest.raises(_lib.FlexAttnError):  # stage counts / q tiles without an instantiation
+            pf.flex_attention(x, x, x, kernel_options=bad)
+    xr = x.detach().requires_grad_()
+    with pytest.raises(_lib.FlexAttnError):  # 128-query dK/dV tiles need 128-key dK/dV workgroups
+        pf.flex_attention(xr, xr, xr, kernel_options={"BLOCK_KV": 64, "BLOCK_Q": 128}).sum().backward()
     q = torch.randn(1, 2, 512, 128, device="cuda", dtype=torch.bfloat16)
     bm = pf.create_block_mask(pf.causal_mask, 1, 2, 512, 512, 128)
     a = pf.flex_attention(q, q, q, block_mask=bm, kernel_options={"BLOCK_M": 256})
