@@ -288,8 +288,9 @@ def main():
                     help="further workloads reported as extra keys (fwd and fwd+bwd TFLOP/s); '' for none")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--profile-kernel", choices=("fwd", "dkdv", "dq", "copy"), default=None,
+    ap.add_argument("--profile-kernel", choices=("fwd", "dkdv", "dq", "bwd", "copy"), default=None,
                     help="run only this kernel --profile-iters times and exit (for rocprofv3 counter passes; "
+                         "bwd = fa_bwd, the dQ kernel with Delta fused then dK/dV; "
                          "copy = a 256 MiB device copy used to calibrate FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--profile-iters", type=int, default=3)
     ap.add_argument("--dense-ref", action="store_true",
@@ -330,7 +331,7 @@ def main():
     if args.profile_kernel:
         runner.fwd()
         runner.preprocess()
-        fn = {"fwd": runner.fwd, "dkdv": runner.dkdv, "dq": runner.dq_}[args.profile_kernel]
+        fn = {"fwd": runner.fwd, "dkdv": runner.dkdv, "dq": runner.dq_, "bwd": runner.bwd}[args.profile_kernel]
         for _ in range(args.profile_iters):
             fn()
         torch.cuda.synchronize()
