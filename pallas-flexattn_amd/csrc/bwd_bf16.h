@@ -464,8 +464,29 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   int qlo, qhi;  // queries that see this lane's key (masks are intervals here)
   query_interval(P, b, kw, &qlo, &qhi);
 
-  RowTile<D> rt;
+  // LDS operand offsets.  ds_read's immediate offset has 16 bits, and the dO
+  // tiles and the statistics lie above 64 KiB: their reads go through lane
+  // offsets that already include the region's start (kept opaque, so the
+  // compiler holds them in registers instead of adding the start before
+  // every read), leaving only tile-relative immediates.
+  RowTile<D> rt, rtd;
   rt.init(lane);
+  rtd.init(lane);
+#pragma unroll
+  for (int s = 0; s < KSTEPS; ++s) {
+    rtd.aoff[s] += 2 * TILE;
+    asm volatile("" : "+v"(rtd.aoff[s]));
+  }
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      rtd.tr[r][t] += 2 * TILE;
+      asm volatile("" : "+v"(rtd.tr[r][t]));
+    }
+  int stat_off = 4 * TILE + 32 * hh;  // + acc_row(e, hh) - acc_row(e, 0), in bytes
+  asm volatile("" : "+v"(stat_off));
+  const char* const statp = lds + stat_off;
   TileDma<D, BQ, NW> dma;
   dma.init(lane, w);
 
@@ -556,7 +577,7 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   // quad due next (Delta is the dP MFMAs' initial value).  Score mods, when
   // present, are evaluated branch-free in the exponential's stage.
   // sched_barrier fences keep the compiler to this order.
-  auto tile_fast = [&](int qbase, int hq, float slope, const char* ql, const char* dl_, const float* lsel,
+  auto tile_fast = [&](int qbase, int hq, float slope, const char* ql, const float* lsel,
                        const float* dltl, auto&& prep, auto&& copy_k, auto&& stat_k, auto masked_c) {
     constexpr bool kMasked = decltype(masked_c)::value;
     constexpr int KS = KSTEPS, NSTEP = 2 * NQS * KS, PF = APF, R = PF + 1;
@@ -609,7 +630,7 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
         zero(sacc[j]);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const f32x4 d4 = *reinterpret_cast<const f32x4*>(dltl + 32 * (2 * u + j) + acc_row(4 * q, hh));
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(dltl + 32 * (2 * u + j) + acc_row(4 * q, 0));
 #pragma unroll
           for (int i = 0; i < 4; ++i) pacc[j][4 * q + i] = d4[i];
         }
@@ -623,15 +644,15 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
       const int ph = t / KS, s = t % KS, u = ph / 4, lph = ph % 4;
       if (lph < 2) {
         ring[t % R][0] = rt.a_frag(ql, 2 * u + lph, s);
-        ring[t % R][1] = rt.a_frag(dl_, 2 * u + lph, s);
+        ring[t % R][1] = rtd.a_frag(ql, 2 * u + lph, s);
       } else {
         const int J = 2 * u + lph - 2;
-        ring[t % R][0] = rt.t_frag(dl_, s >> 1, 2 * J + (s & 1));
+        ring[t % R][0] = rtd.t_frag(ql, s >> 1, 2 * J + (s & 1));
         ring[t % R][1] = rt.t_frag(ql, s >> 1, 2 * J + (s & 1));
       }
     };
     auto load_stats = [&](int J, int q) {
-      const int r0 = 32 * J + acc_row(4 * q, hh);
+      const int r0 = 32 * J + acc_row(4 * q, 0);
       ls[J & 1][q] = *reinterpret_cast<const f32x4*>(lsel + r0);
     };
     // A pair's E work in two stages a step apart, so the exponentials'
@@ -784,7 +805,15 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   // table lookups and the first tile's copy.)
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int s = 0; s < KSTEPS; ++s) vf[s] ^= 0x80008000u;
+  for (int s = 0; s < KSTEPS; ++s) {
+    vf[s] ^= 0x80008000u;
+    // K and V live in AGPRs (the S and dP MFMAs read their B operand from
+    // there): beside the dK / dV accumulators the AGPR file has 128 registers
+    // left, and the 64 VGPRs this frees hold the LDS offsets of the dO and
+    // statistics reads (about 70 VALU instructions fewer per q tile).
+    asm volatile("" : "+a"(vf[s]));
+    asm volatile("" : "+a"(kf[s]));
+  }
   auto step = [&](int it, auto masked_c, auto buf_c) {
     constexpr int buf = decltype(buf_c)::value;  // == it & 1, a constant (immediate LDS offsets)
     const int hq = hq_next, qbase = qb_next;
@@ -806,9 +835,9 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
     auto fetch_next = [&]() { ref_next = walk.fetch(min(it + 2, n_it - 1)); };
     if (qbase < P.Sq) {
       const float slope = (kMods && P.alibi) ? P.alibi[hq] : 0.f;
-      tile_fast(qbase, hq, slope, lds + buf * TILE, lds + (2 + buf) * TILE,
-                reinterpret_cast<const float*>(lds + 4 * TILE + buf * STAT),
-                reinterpret_cast<const float*>(lds + 4 * TILE + (2 + buf) * STAT), prep, copy_k, stat_k,
+      tile_fast(qbase, hq, slope, lds + buf * TILE,
+                reinterpret_cast<const float*>(statp + buf * STAT),
+                reinterpret_cast<const float*>(statp + (2 + buf) * STAT), prep, copy_k, stat_k,
                 masked_c);
       fetch_next();
     } else {
