@@ -20,7 +20,11 @@ roofline of the dominant kernel (HIP events on the launch stream; HBM bytes
 per launch from profiles/traffic.json only when that file was measured on the
 current kernel sources) and the CPU baseline: the oracle's C restatement of
 the reference's tiled algorithm, timed on a bounded sample of heads of the
-same workload on this host.
+same workload on this host.  ``gemm_reference`` times torch's bf16 GEMM
+(hipBLASLt, 8192^3) on the same GPU in the same run: the board runs at its
+power limit under sustained matrix-core load, so that figure is the practical
+ceiling the attention figures are read against.  ``--power`` samples socket
+power and GFX clocks (amd-smi) while each kernel runs back to back.
 """
 import argparse
 import json
@@ -223,6 +227,90 @@ def sources_sha256():
     return h.hexdigest()
 
 
+def gemm_reference(steps, stream):
+    """The bf16 GEMM torch runs through hipBLASLt, 8192 x 8192 x 8192, timed the
+    same way on the same GPU: what a plain library GEMM reaches on this board
+    under its power limit, next to the attention kernels."""
+    import torch
+    n = 8192
+    a = torch.randn(n, n, device="cuda", dtype=torch.bfloat16)
+    b = torch.randn(n, n, device="cuda", dtype=torch.bfloat16)
+    c = torch.empty(n, n, device="cuda", dtype=torch.bfloat16)
+    fn = lambda: torch.matmul(a, b, out=c)  # noqa: E731
+    warm(fn, min_s=0.2)
+    ms = time_region(fn, steps, stream)
+    tf = 2.0 * n ** 3 / (ms * 1e-3) / 1e12
+    return {"workload": "bf16 GEMM 8192 x 8192 x 8192 (torch.matmul, hipBLASLt)", "ms": round(ms, 4),
+            "tflops": round(tf, 2), "pct_peak": round(100 * tf / PEAK_BF16_TFLOPS, 2)}
+
+
+def amd_smi_sample():
+    """(socket power W, mean GFX clock MHz over the XCDs) from one amd-smi
+    reading, or None."""
+    import re
+    import subprocess
+    try:
+        out = subprocess.run(["amd-smi", "metric", "-p", "-c"], capture_output=True, text=True, timeout=10).stdout
+    except (OSError, subprocess.SubprocessError):
+        return None
+    pw = re.search(r"SOCKET_POWER:\s*([0-9.]+)\s*W", out)
+    clks, in_gfx = [], False
+    for line in out.splitlines():
+        t = line.strip()
+        if re.match(r"GFX_\d+:", t):
+            in_gfx = True
+        elif in_gfx and t.startswith("CLK:"):
+            m = re.match(r"CLK:\s*([0-9.]+)\s*MHz", t)
+            if m:
+                clks.append(float(m.group(1)))
+            in_gfx = False
+    if not pw or not clks:
+        return None
+    return float(pw.group(1)), sum(clks) / len(clks)
+
+
+def power_profile(fns, seconds=2.5):
+    """Runs each (name, fn) back to back for `seconds` while amd-smi samples the
+    socket power and GFX clocks; the first 0.8 s (clock ramp) is left out.
+    Returns {name: {"watts": median, "mhz": median, "samples": n, "ms": per call}}."""
+    import threading
+    import torch
+    res = {}
+    for name, fn in fns:
+        samples, stop = [], [False]
+
+        def sampler():
+            while not stop[0]:
+                t = time.perf_counter()
+                s = amd_smi_sample()
+                if s is not None:
+                    samples.append((t, s))
+                time.sleep(0.05)
+
+        th = threading.Thread(target=sampler)
+        t0 = time.perf_counter()
+        th.start()
+        n = 0
+        while time.perf_counter() - t0 < seconds:
+            fn()
+            n += 1
+            if n % 4 == 0:
+                torch.cuda.synchronize()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        stop[0] = True
+        th.join()
+        vals = [s for t, s in samples if t0 + 0.8 < t < t1]
+        if vals:
+            w = sorted(v[0] for v in vals)[len(vals) // 2]
+            mhz = sorted(v[1] for v in vals)[len(vals) // 2]
+            res[name] = {"watts": w, "mhz": round(mhz), "samples": len(vals), "ms": round((t1 - t0) * 1e3 / n, 4)}
+        else:
+            res[name] = {"watts": None, "mhz": None, "samples": 0, "ms": round((t1 - t0) * 1e3 / n, 4)}
+        log(f"power {name}: {res[name]}")
+    return res
+
+
 def measured_traffic(config, kernel):
     """HBM bytes per launch of `kernel` at `config` from profiles/traffic.json,
     only if it was measured on the current kernel sources (else None)."""
@@ -293,6 +381,9 @@ def main():
                          "bwd = fa_bwd, the dQ kernel with Delta fused then dK/dV; "
                          "copy = a 256 MiB device copy used to calibrate FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--profile-iters", type=int, default=3)
+    ap.add_argument("--power", action="store_true",
+                    help="run the forward, dK/dV, dQ, the whole step and a bf16 GEMM back to back for a few "
+                         "seconds each while amd-smi samples socket power and GFX clocks; print them and exit")
     ap.add_argument("--dense-ref", action="store_true",
                     help="also time the headline shape with no mask (every tile live) and report the time "
                          "fraction next to the live-block fraction (sparse-proportionality check)")
@@ -328,6 +419,28 @@ def main():
     flop_fwd = 4.0 * D * pairs * Hq
     flop_bwd = 10.0 * D * pairs * Hq
 
+    if args.power:
+        import torch
+        n = 8192
+        ga = torch.randn(n, n, device="cuda", dtype=torch.bfloat16)
+        gb = torch.randn(n, n, device="cuda", dtype=torch.bfloat16)
+        gc = torch.empty(n, n, device="cuda", dtype=torch.bfloat16)
+        runner.fwd()
+        runner.preprocess()
+        idle = [amd_smi_sample() for _ in range(5)]
+        idle = [x for x in idle if x]
+        res = power_profile((("fwd", runner.fwd), ("bwd_dkdv", runner.dkdv), ("bwd_dq", runner.dq_),
+                             ("step", runner.step), ("gemm_bf16_8192", lambda: torch.matmul(ga, gb, out=gc))))
+        flops = {"fwd": flop_fwd, "bwd_dkdv": 8.0 * D * pairs * Hq, "bwd_dq": 6.0 * D * pairs * Hq,
+                 "step": flop_fwd + flop_bwd, "gemm_bf16_8192": 2.0 * n ** 3}
+        for k, v in res.items():
+            v["tflops"] = round(flops[k] / (v["ms"] * 1e-3) / 1e12, 1)
+            v["pct_peak"] = round(100 * v["tflops"] / PEAK_BF16_TFLOPS, 2)
+        print(json.dumps({"config": cfg["workload"], "idle": {"watts": idle[0][0] if idle else None,
+                                                              "mhz": round(idle[0][1]) if idle else None},
+                          "kernels": res}))
+        return
+
     if args.profile_kernel:
         runner.fwd()
         runner.preprocess()
@@ -354,30 +467,20 @@ def main():
                          "full_kv_indices", "q_num_blocks", "q_indices", "full_q_num_blocks", "full_q_indices")):
         raise SystemExit("device and host block masks differ")
 
-    if args.warmup is None:
-        args.warmup = warm(runner.step)
-    else:
-        for _ in range(args.warmup):
-            runner.step()
-    torch.cuda.synchronize()
-    log(f"warmup done ({args.warmup} steps)")
-    ms_step = time_region(runner.step, args.steps, stream)
-    torch.cuda.synchronize()
-    log(f"timed {args.steps} steps: {ms_step:.3f} ms/step")
-
     # per-kernel times: the forward, the whole backward, and the staged
-    # kernels (Delta pass, dK/dV, dQ reading Delta); the dQ kernel with
-    # Delta fused takes about bwd - bwd_dkdv
+    # kernels (Delta pass, dK/dV, dQ reading Delta), each after its own short
+    # warm-up; the dQ kernel with Delta fused takes about bwd - bwd_dkdv.
+    # They run before the headline steps, so those start on a GPU whose clock
+    # has left its idle state, as in a training loop.
     kernels = {}
     for name, fn in (("fwd", runner.fwd), ("bwd", runner.bwd), ("bwd_preprocess", runner.preprocess),
                      ("bwd_dkdv", runner.dkdv), ("bwd_dq", runner.dq_)):
-        fn()
+        warm(fn, min_steps=2, min_s=0.05)
         kernels[name] = time_region(fn, args.steps, stream)
     ms_fwd = kernels["fwd"]
     algo = {"fwd": flop_fwd, "bwd_dkdv": 8.0 * D * pairs * Hq, "bwd_dq": 6.0 * D * pairs * Hq}
     dom = max(("fwd", "bwd_dkdv", "bwd_dq"), key=lambda n: kernels[n])
     achieved = algo[dom] / (kernels[dom] * 1e-3) / 1e12
-    fwdbwd_tflops = (flop_fwd + flop_bwd) / (ms_step * 1e-3) / 1e12
     fwd_tflops = flop_fwd / (ms_fwd * 1e-3) / 1e12
 
     # the public API on the same inputs: flex_attention forward + autograd
@@ -390,8 +493,21 @@ def main():
 
     warm(api_step, min_s=0.1)
     api_ms = time_region(api_step, args.steps, stream)
-    log(f"flex_attention fwd+bwd: {api_ms:.3f} ms/step (Runner {ms_step:.3f})")
     del qq, kk, vv
+
+    # the headline: W untimed steps, then exactly K timed steps
+    if args.warmup is None:
+        args.warmup = warm(runner.step)
+    else:
+        for _ in range(args.warmup):
+            runner.step()
+    torch.cuda.synchronize()
+    log(f"warmup done ({args.warmup} steps)")
+    ms_step = time_region(runner.step, args.steps, stream)
+    torch.cuda.synchronize()
+    log(f"timed {args.steps} steps: {ms_step:.3f} ms/step")
+    fwdbwd_tflops = (flop_fwd + flop_bwd) / (ms_step * 1e-3) / 1e12
+    log(f"flex_attention fwd+bwd: {api_ms:.3f} ms/step (Runner {ms_step:.3f})")
 
     # the fp8 forward on the same workload: q, k, v quantised once (timed
     # apart), then the fp8 kernel alone, inputs resident in HBM
@@ -454,6 +570,9 @@ def main():
         del orun, obm
         torch.cuda.empty_cache()
 
+    gemm = gemm_reference(args.steps, stream) if not args.profile_kernel else None
+    log(f"bf16 GEMM reference: {gemm['tflops']} TFLOP/s ({gemm['pct_peak']} % of peak)")
+
     out = {
         "metric": METRIC,
         "value": round(fwdbwd_tflops, 2),
@@ -485,6 +604,7 @@ def main():
         "cpu_baseline": cpu,
         "fp8_forward": fp8,
         "other_configs": others,
+        "gemm_reference": gemm,
     }
     if sparsity is not None:
         out["sparsity_check"] = sparsity
