@@ -578,9 +578,13 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
   // present, are evaluated branch-free in the exponential's stage.
   // sched_barrier fences keep the compiler to this order.
   auto tile_fast = [&](int qbase, int hq, float slope, const char* ql, const float* lsel,
-                       const float* dltl, auto&& prep, auto&& copy_k, auto&& stat_k, auto masked_c) {
+                       const float* dltl, auto&& prep, auto&& copy_k, auto&& stat_k, auto&& fetch_k,
+                       auto masked_c) {
     constexpr bool kMasked = decltype(masked_c)::value;
     constexpr int KS = KSTEPS, NSTEP = 2 * NQS * KS, PF = APF, R = PF + 1;
+    // first step of the last pair's A0 phase (steps with no E work; for a
+    // single pair, the first step of C1)
+    constexpr int kFetchStep = NQS > 2 ? 4 * KS * (NQS / 2 - 1) + 1 : 3 * KS + 1;
     static_assert(NDMA + 1 < NSTEP, "the next tile's copies fit the steps before its LSE store");
     static_assert(2 * DT == KS && NQS % 2 == 0, "fast path shape");
     // Partial tiles: element e of sub-tile J is query qbase + 32 J + 8 hh +
@@ -636,7 +640,6 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
         }
       }
     };
-    init_pair(0);
     frag pf[2][2], sf[2][2];
     frag ring[R][2];
     f32x4 ls[2][4];
@@ -731,6 +734,7 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
         asm volatile("s_nop 1" : "+v"(pf[j][half]), "+v"(sf[j][half]));
       }
     };
+    init_pair(0);
 #pragma unroll
     for (int t = 0; t < PF; ++t) load(t);
     // the next tile's walk and copy plan (scalar work) while the first
@@ -776,6 +780,11 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
       // the next tile's copies, one per step; its LSE stored near the end
       if (t < NDMA) copy_k(t);
       if (t == NSTEP - 2) stat_k();
+      // the table entry of the tile after next: its scalar work runs beside
+      // the MFMAs of a step with no exponentials or copies, its load passes
+      // under the rest of the tile (at the tile's end all four waves would
+      // run it on the shared scalar unit at once)
+      if (t == kFetchStep) fetch_k();
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -838,8 +847,7 @@ __global__ __launch_bounds__(NW * 64) void dkdv_bf16_kernel(BwdArgs a) {
       tile_fast(qbase, hq, slope, lds + buf * TILE,
                 reinterpret_cast<const float*>(statp + buf * STAT),
                 reinterpret_cast<const float*>(statp + (2 + buf) * STAT), prep, copy_k, stat_k,
-                masked_c);
-      fetch_next();
+                fetch_next, masked_c);
     } else {
       prep();
 #pragma unroll

@@ -339,6 +339,16 @@ struct QWalkT {
   FA_HD TileRef fetch(int it) const {
     const int part = it >= n_full ? 1 : 0;
     int gi = 0, rem = part ? it - n_full : it;
+    if (g == 1 && sub == 1) {
+      // one q head and one q tile per mask block (the common layout): the
+      // entry is the list word itself.  Same result as the general path
+      // below, without its head and sub-tile arithmetic, which the four
+      // waves of a workgroup would run on the shared scalar unit at the same
+      // moment at every tile boundary.
+      TileRef r{rem, 0, hq0};
+      if (!dense) r.raw = part ? L::vector(pl0, rem, np0) : L::vector(fl0, rem, nf0);
+      return r;
+    }
     int nf = nf0, np = np0;
     const int *fl = fl0, *pl = pl0;
     if (dense || P->tab_h == 1) {
