@@ -374,14 +374,21 @@ void dq_bf16_kernel(BwdArgs a) {
     const int kbase = kb_next;
     const bool more = it + 1 < n_it;
     i32x4 rk = {0, 0, 0, 0}, rv = {0, 0, 0, 0};
-    if (more) {
-      kb_next = walk.kbase(ref_next);
-      rk = TileDma<D, BN, NW>::rsrc(kbase_ptr, kb_next, P.Skv);
-      rv = TileDma<D, BN, NW>::rsrc(vbase_ptr, kb_next, P.Skv);
-    }
+    // the next tile's start and copy resources, and the table entry of the
+    // tile after it: scalar work, run behind the tile's first MFMAs (before
+    // them, the workgroup's waves would run it on the shared scalar unit at
+    // once while their matrix cores wait)
+    auto prep = [&]() {
+      if (more) {
+        kb_next = walk.kbase(ref_next);
+        rk = TileDma<D, BN, NW>::rsrc(kbase_ptr, kb_next, P.Skv);
+        rv = TileDma<D, BN, NW>::rsrc(vbase_ptr, kb_next, P.Skv);
+      }
+      if (it + 2 < n_it) ref_next = walk.fetch(it + 2);
+    };
     char* nk = lds + (buf ^ 1) * TILE;
     char* nv = lds + (2 + (buf ^ 1)) * TILE;
-    auto copies = [&](int s) {
+    auto issue_copies = [&](int s) {
 #pragma unroll
       for (int i = 0; i < 2 * IPW; ++i)
         if (i * KSTEPS / (2 * IPW) == s && more) {
@@ -389,12 +396,16 @@ void dq_bf16_kernel(BwdArgs a) {
           else dma.one(rv, i - IPW, nv, w);
         }
     };
-    if (it + 2 < n_it) ref_next = walk.fetch(it + 2);
+    auto copies = [&](int s) {
+      if (s == 0) prep();
+      issue_copies(s);
+    };
     if (kbase < P.Skv) {
       tile(kbase, lds + buf * TILE, lds + (2 + buf) * TILE, masked_c, copies);
     } else {
+      prep();
 #pragma unroll
-      for (int s = 0; s < KSTEPS; ++s) copies(s);
+      for (int s = 0; s < KSTEPS; ++s) issue_copies(s);
     }
     wait_vmem();
     __syncthreads();
