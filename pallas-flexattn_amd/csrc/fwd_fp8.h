@@ -401,34 +401,64 @@ struct QuantArgs {
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
 
+// 4 x 4 byte transpose: o[c] byte r = byte c of word r (v_perm_b32 picks
+// bytes of {S0, S1}, selector values 0-3 from S1, 4-7 from S0)
+__device__ __forceinline__ void transpose_bytes4(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, uint32_t* o) {
+  const uint32_t t0 = __builtin_amdgcn_perm(w1, w0, 0x05010400u);  // w0.b0 w1.b0 w0.b1 w1.b1
+  const uint32_t t1 = __builtin_amdgcn_perm(w1, w0, 0x07030602u);  // w0.b2 w1.b2 w0.b3 w1.b3
+  const uint32_t t2 = __builtin_amdgcn_perm(w3, w2, 0x05010400u);
+  const uint32_t t3 = __builtin_amdgcn_perm(w3, w2, 0x07030602u);
+  o[0] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
+  o[1] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
+  o[2] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
+  o[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
+}
+
+// One pass over the block: each working thread holds eight 16-byte chunks
+// (64 values) in registers from the load through the block maximum to the
+// conversion.  Row-major output: chunk tid + NT j of the block, stored as 8
+// bytes.  Transposed output: rows 8 g .. 8 g + 7 of chunk c (g = tid % 16,
+// c = tid / 16), the 8 x 8 bytes transposed in registers and stored as 8
+// bytes of each of the chunk's 8 V^T rows (16 lanes fill a 128-byte row).
 template <int D>
 __global__ __launch_bounds__(256) void quant_fp8_kernel(QuantArgs a) {
   constexpr int R = kFp8ScaleRows;
-  __shared__ float red[256];
-  __shared__ __attribute__((aligned(16))) uint8_t tile[R * D];  // e4m3 block, row-major
+  constexpr int NCH = D / 8;         // 16-byte chunks per row
+  constexpr int NT = R * NCH / 8;    // threads with work (8 chunks each): 256, 128, 64
+  static_assert(R == 128 && NT <= 256 && NT == 16 * NCH, "block shape");
+  __shared__ float red[4];
   const int nb = (a.S + R - 1) / R;
   const int head = blockIdx.x / nb, blk = blockIdx.x - head * nb;
   const int r0 = blk * R;
   const int rows = min(R, a.S - r0);
   const uint16_t* src = a.x + ((size_t)head * a.S + r0) * D;
   const int tid = threadIdx.x;
-  // amax over the block (8 elements per 16-byte load)
+  const bool tr = a.transpose != 0;
+  const bool act = tid < NT;
+  const int g = tid & 15, c = tid >> 4;
+  auto row_of = [&](int j) { return tr ? 8 * g + j : (tid + NT * j) / NCH; };
+  auto chunk_of = [&](int j) { return tr ? c : (tid + NT * j) % NCH; };
+  u32x4 v[8];
   float amax = 0.f;
-  for (int i = tid; i < rows * D / 8; i += 256) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(src + i * 8);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int r = row_of(j);
+    v[j] = u32x4{0u, 0u, 0u, 0u};
+    if (act && r < rows) v[j] = *reinterpret_cast<const u32x4*>(src + r * D + chunk_of(j) * 8);
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      amax = fmaxf(amax, fabsf(__uint_as_float(v[t] << 16)));
-      amax = fmaxf(amax, fabsf(__uint_as_float(v[t] & 0xffff0000u)));
+      amax = fmaxf(amax, fabsf(__uint_as_float(v[j][t] << 16)));
+      amax = fmaxf(amax, fabsf(__uint_as_float(v[j][t] & 0xffff0000u)));
     }
-  }
-  red[tid] = amax;
+  // block maximum: across the wave, then the four waves
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  if ((tid & 63) == 0) red[tid >> 6] = amax;
   __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if (tid < s) red[tid] = fmaxf(red[tid], red[tid + s]);
-    __syncthreads();
-  }
-  amax = red[0];
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   // smallest e with 448 * 2^e >= amax (frexp-style on the ratio, exact)
   // (clamped to [-126, 127]: the scale stays a normal float, whose exponent
   // field is its E8M0 code; a non-finite amax leaves scale 1)
@@ -441,38 +471,41 @@ __global__ __launch_bounds__(256) void quant_fp8_kernel(QuantArgs a) {
   }
   const float inv = ldexpf(1.0f, -e);
   if (tid == 0) a.scale[(size_t)head * nb + blk] = ldexpf(1.0f, e);
-  // convert (rows past S are zero)
-  for (int i = tid; i < R * D / 4; i += 256) {
-    const int r = (i * 4) / D;
-    float x[4] = {0.f, 0.f, 0.f, 0.f};
-    if (r < rows) {
-      const u32x2 v = *reinterpret_cast<const u32x2*>(src + i * 4);
-      x[0] = __uint_as_float(v[0] << 16) * inv;
-      x[1] = __uint_as_float(v[0] & 0xffff0000u) * inv;
-      x[2] = __uint_as_float(v[1] << 16) * inv;
-      x[3] = __uint_as_float(v[1] & 0xffff0000u) * inv;
-    }
-    int word = __builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false);
-    word = __builtin_amdgcn_cvt_pk_fp8_f32(x[2], x[3], word, true);
-    if (a.transpose) *reinterpret_cast<int*>(tile + i * 4) = word;
-    else if (r < rows) *reinterpret_cast<int*>(a.out + ((size_t)head * a.S + r0) * D + i * 4) = word;
-  }
-  if (!a.transpose) return;
-  __syncthreads();
-  // V^T: row d of the block = column d of the tile, R bytes (16 per thread step)
-  uint8_t* dst = a.out + (size_t)head * D * a.ld + r0;
-  for (int i = tid; i < D * (R / 16); i += 256) {
-    const int d = i / (R / 16), c = i - d * (R / 16);
-    u32x4 v;
+  if (!act) return;
+  // convert (rows past S are zero): lo = values 0-3 of the chunk, hi = 4-7
+  uint32_t lo[8], hi[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    float x[8];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      uint32_t wv = 0;
-#pragma unroll
-      for (int bq = 0; bq < 4; ++bq) wv |= (uint32_t)tile[(16 * c + 4 * t + bq) * D + d] << (8 * bq);
-      v[t] = wv;
+      x[2 * t] = __uint_as_float(v[j][t] << 16) * inv;
+      x[2 * t + 1] = __uint_as_float(v[j][t] & 0xffff0000u) * inv;
     }
-    *reinterpret_cast<u32x4*>(dst + (size_t)d * a.ld + 16 * c) = v;
+    int w0 = __builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false);
+    w0 = __builtin_amdgcn_cvt_pk_fp8_f32(x[2], x[3], w0, true);
+    int w1 = __builtin_amdgcn_cvt_pk_fp8_f32(x[4], x[5], 0, false);
+    w1 = __builtin_amdgcn_cvt_pk_fp8_f32(x[6], x[7], w1, true);
+    lo[j] = (uint32_t)w0;
+    hi[j] = (uint32_t)w1;
   }
+  if (!tr) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int r = row_of(j);
+      if (r < rows) *reinterpret_cast<u32x2*>(a.out + ((size_t)head * a.S + r0 + r) * D + chunk_of(j) * 8) = u32x2{lo[j], hi[j]};
+    }
+    return;
+  }
+  // V^T: row d = 8 c + k of the block holds bytes k of rows 8 g .. 8 g + 7
+  uint32_t tl[8], th[8];  // tl[k]: rows 8g..8g+3 of head-dim index 8c + k, th[k]: rows 8g+4..8g+7
+  transpose_bytes4(lo[0], lo[1], lo[2], lo[3], tl);
+  transpose_bytes4(lo[4], lo[5], lo[6], lo[7], th);
+  transpose_bytes4(hi[0], hi[1], hi[2], hi[3], tl + 4);
+  transpose_bytes4(hi[4], hi[5], hi[6], hi[7], th + 4);
+  uint8_t* dst = a.out + ((size_t)head * D + 8 * c) * a.ld + r0 + 8 * g;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) *reinterpret_cast<u32x2*>(dst + (size_t)k * a.ld) = u32x2{tl[k], th[k]};
 }
 
 }  // namespace fa
